@@ -1,0 +1,264 @@
+"""Pins the CPU oracle before anything is checked against it (CPU only).
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped term, a swapped nibble, a wrong tie order,
+an off-by-one draw) fails: fixtures from the compiled reference (tests/golden/make_golden.py), brute force, basis
+vectors, and sorts done a different way than the oracle does them.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import util
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    if not os.path.exists(orc.ORACLE_SO):
+        orc.build()
+
+
+# ---------------- formats (a1 / a2) ----------------
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("G", [32, 64, 128])
+def test_dequant_matches_reference_fixture(golden_dir, bits, G):
+    f = np.load(os.path.join(golden_dir, "formats.npz"))
+    tag = f"q{bits}_g{G}"
+    N, K = f[tag + "_w"].shape
+    w = orc.QWeight(bits, f[tag + "_q"], f[tag + "_scale"], f[tag + "_min"], N, K, G)
+    got = orc.dequant(w)
+    assert np.array_equal(got.view(np.uint32), f[tag + "_deq"].view(np.uint32))  # bit-exact
+
+
+@pytest.mark.skipif(not orc.ref_available(), reason="oracle/_ref not built (needs the reference tree)")
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_matches_live_reference_random_codes(bits):
+    w = util.rand_qweight(np.random.default_rng(5), bits, 16, 512, 64)
+    assert np.array_equal(orc.dequant(w).view(np.uint32), orc.ref_dequantize(w).view(np.uint32))
+
+
+def test_dequant_nibble_order():
+    # formats/q4.hpp:4: low nibble = even k. Byte 0x21 -> codes 1 (k=0), 2 (k=1); scale 1, min 0.
+    q = np.zeros(64, np.uint8)
+    q[0] = 0x21
+    one = np.array([0x3F80], np.uint16)
+    w = orc.QWeight(4, q, np.repeat(one, 1), np.zeros(1, np.uint16), 1, 128, 128)
+    d = orc.dequant(w)
+    assert d[0, 0] == 1.0 and d[0, 1] == 2.0 and np.all(d[0, 2:] == 0)
+
+
+# ---------------- dense linear (a3 / a4) ----------------
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_linear_brute_force(bits):
+    rng = np.random.default_rng(6)
+    w = util.rand_qweight(rng, bits, 40, 256, 32)
+    x = rng.standard_normal((3, 256)).astype(np.float32)
+    y = orc.linear_q(x, w)
+    ref = x.astype(np.float64) @ orc.dequant(w).astype(np.float64).T
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_linear_basis_vectors_recover_weights(bits):
+    rng = np.random.default_rng(7)
+    w = util.rand_qweight(rng, bits, 8, 128, 64)
+    d = orc.dequant(w)
+    for k in (0, 1, 63, 64, 127):
+        x = np.zeros((1, 128), np.float32)
+        x[0, k] = 1.0
+        assert np.array_equal(orc.linear_q(x, w)[0], d[:, k])
+        xb = util.f32_to_bf16(x)  # bf16 path: the same column, then rounded once to bf16
+        assert np.array_equal(orc.linear_q(xb, w)[0], util.f32_to_bf16(d[:, k]))
+
+
+def test_linear_bf16_to_f32_rowsums():
+    rng = np.random.default_rng(8)
+    w = util.rand_qweight(rng, 4, 5, 256, 128)
+    x = util.f32_to_bf16(np.ones((2, 256), np.float32))
+    y = orc.linear_q(x, w, out_act=orc.F32)
+    np.testing.assert_allclose(y, np.tile(orc.dequant(w).astype(np.float64).sum(1), (2, 1)), rtol=1e-6)
+
+
+# ---------------- router (a5) ----------------
+
+def _router_by_lexsort(logits, k):
+    M, E = logits.shape
+    ids = np.empty((M, k), np.int32)
+    for m in range(M):
+        order = np.lexsort((np.arange(E), -logits[m]))  # value desc, then index asc
+        ids[m] = order[:k]
+    return ids
+
+
+def test_router_topk_and_softmax():
+    rng = np.random.default_rng(9)
+    L = rng.standard_normal((7, 512)).astype(np.float32)
+    L[2, 10] = L[2, 400] = L[2, 77] = 5.0  # three-way tie at the top
+    L[4, :] = 0.25                            # all tied: ids 0..k-1
+    ids, coef, err = orc.moe_router(L, 512, 10)
+    assert err[0] == 0
+    assert np.array_equal(ids, _router_by_lexsort(L, 10))
+    assert list(ids[2, :3]) == [10, 77, 400] and list(ids[4]) == list(range(10))
+    for m in range(7):
+        e = np.exp(L[m, ids[m]].astype(np.float64) - L[m, ids[m][0]])
+        np.testing.assert_allclose(coef[m], e / e.sum(), rtol=1e-6)
+
+
+def test_router_nonfinite_and_shared():
+    L = np.random.default_rng(10).standard_normal((3, 64)).astype(np.float32)
+    L[1, 20] = np.inf
+    L[1, 30] = np.nan
+    shared = np.array([0.5, 0.0, -1.0], np.float32)
+    ids, coef, err = orc.moe_router(L, 64, 4, shared=shared, shared_ld=1, shared_id=64)
+    assert list(err) == [1, 1, 20]
+    assert np.all(ids[1] == -1) and np.all(np.isnan(coef[1]))
+    assert ids[0, 4] == 64 and abs(coef[0, 4] - 1 / (1 + np.exp(-0.5))) < 1e-7
+    ids, coef, err = orc.moe_router(np.array([[3.0]], np.float32), 1, 1)
+    assert ids[0, 0] == 0 and coef[0, 0] == 1.0
+
+
+# ---------------- experts (a6 / a9) ----------------
+
+def test_experts_gather_swiglu_combine_compose():
+    rng = np.random.default_rng(11)
+    E, I, K = 6, 32, 128
+    wgu = util.rand_qweight(rng, 4, E * 2 * I, K, 64)
+    wdn = util.rand_qweight(rng, 4, E * K, I, 32)
+    x = util.f32_to_bf16(rng.standard_normal((3, K)).astype(np.float32))
+    ids = np.array([[0, 5], [2, 2], [5, 1]], np.int32)
+    coef = np.array([[0.7, 0.3], [0.5, 0.5], [0.1, 0.9]], np.float32)
+    gu, err = orc.experts_gather(x, wgu, E, ids)
+    assert err[0] == 0
+    h, _ = orc.experts_gather(x, wgu, E, ids, swiglu=True)
+    assert np.array_equal(h, orc.swiglu(gu.reshape(6, 2 * I)).reshape(3, 2, I))  # bit-identical composition
+    # gather of one slot = the dense linear on that expert's rows
+    e = 2
+    sub = orc.QWeight(4, wgu.q.reshape(E * 2 * I, -1)[e * 2 * I:(e + 1) * 2 * I].ravel(),
+                      wgu.scale.reshape(E * 2 * I, -1)[e * 2 * I:(e + 1) * 2 * I].ravel(),
+                      wgu.minv.reshape(E * 2 * I, -1)[e * 2 * I:(e + 1) * 2 * I].ravel(), 2 * I, K, 64)
+    assert np.array_equal(gu[1, 0], orc.linear_q(x[1:2], sub)[0])
+    y, err = orc.experts_combine(h, wdn, E, ids, coef)
+    dd = orc.dequant(wdn).astype(np.float64).reshape(E, K, I)
+    hf = util.bf16_to_f32(h).astype(np.float64)
+    ref = np.stack([sum(coef[m, a] * dd[ids[m, a]] @ hf[m, a] for a in range(2)) for m in range(3)])
+    np.testing.assert_allclose(util.bf16_to_f32(y), ref, rtol=8e-3, atol=1e-3 * np.abs(ref).max())
+
+
+def test_experts_bad_id():
+    rng = np.random.default_rng(12)
+    w = util.rand_qweight(rng, 4, 4 * 8, 64, 32)
+    x = rng.standard_normal((2, 64)).astype(np.float32)
+    ids = np.array([[1, 7], [0, 2]], np.int32)
+    y, err = orc.experts_gather(x, w, 4, ids)
+    assert list(err) == [1, 7, 1] and np.all(np.isnan(y[0, 1])) and not np.any(np.isnan(y[1]))
+    wd = util.rand_qweight(rng, 4, 4 * 16, 32, 32)
+    y, err = orc.experts_combine(np.ones((2, 2, 32), np.float32), wd, 4, ids, np.ones((2, 2), np.float32))
+    assert list(err) == [1, 7, 1] and np.all(np.isnan(y[0])) and not np.any(np.isnan(y[1]))
+
+
+# ---------------- logits top-k (a10) ----------------
+
+def _topk_by_lexsort(row, n_valid, k, allowed=None):
+    idx = np.arange(n_valid)
+    v = row[:n_valid]
+    keep = ~np.isnan(v)
+    if allowed is not None:
+        keep &= allowed[:n_valid]
+    idx, v = idx[keep], v[keep]
+    order = np.lexsort((idx, -v.astype(np.float64)))[:k]
+    return idx[order]
+
+
+@pytest.mark.parametrize("k", [20, 40])
+def test_logits_topk(k):
+    rng = np.random.default_rng(13)
+    L = rng.standard_normal((5, 3000)).astype(np.float32)
+    L[1, 100:200] = 7.0                # many ties: the lowest ids
+    L[2, 5] = np.nan                   # flagged, left out
+    L[3, :] = -0.0
+    L[3, 50] = 0.0                     # -0 == +0: ids ascending
+    v, i, nan = orc.logits_topk(L, 2900, k)
+    assert list(nan) == [0, 0, 1, 0, 0]
+    for r in range(5):
+        assert np.array_equal(i[r], _topk_by_lexsort(L[r], 2900, k))
+        assert np.array_equal(v[r].view(np.uint32), L[r, i[r]].view(np.uint32))
+    v, i, nan = orc.logits_topk(L[:, :10], 7, k)  # fewer valid than k: padding
+    assert np.all(i[:, 7:] == np.iinfo(np.int32).max) and np.all(v[:, 7:] == -np.inf)
+
+
+def test_logits_topk_mask():
+    rng = np.random.default_rng(14)
+    L = rng.standard_normal((2, 256)).astype(np.float32)
+    allowed = rng.random((2, 256)) < 0.05
+    mask = np.zeros((2, 8), np.uint32)
+    for r in range(2):
+        for j in np.nonzero(allowed[r])[0]:
+            mask[r, j >> 5] |= np.uint32(1 << (j & 31))
+    v, i, nan = orc.logits_topk(L, 256, 20, mask=mask)
+    for r in range(2):
+        exp = _topk_by_lexsort(L[r], 256, 20, allowed[r])
+        assert np.array_equal(i[r, :len(exp)], exp)
+        assert np.all(i[r, len(exp):] == np.iinfo(np.int32).max)
+
+
+# ---------------- top2 (a11) ----------------
+
+def test_top2_matches_reference_fixture(golden_dir):
+    f = np.load(os.path.join(golden_dir, "top2.npz"))
+    for x, n, e in zip(f["x"], f["n"], f["expect"]):
+        b, bv, sv, nan = orc.top2(x[:n])
+        assert (b, nan) == (int(e[0]), int(e[3]))
+        assert np.float32(bv) == np.float32(e[1]) and np.float32(sv) == np.float32(e[2])
+
+
+# ---------------- sampler + accept (a12) ----------------
+
+def test_sampler_matches_reference_fixture(golden_dir):
+    f = np.load(os.path.join(golden_dir, "sampler.npz"))
+    for pi, (T, k, p, seed) in enumerate(f["params"]):
+        X = f[f"x{pi}"]
+        rng = orc.Rng(int(seed))
+        got = [orc.sample_row(rng, X[r], X.shape[1], T, int(k), p) for r in range(X.shape[0])]
+        assert got == list(f[f"ids{pi}"]), (T, k, p)
+        if f"cand_ids{pi}" in f:  # sampling from the top 20 candidates gives the same ids (logits_topk's contract)
+            assert list(f[f"cand_ids{pi}"]) == list(f[f"ids{pi}"])
+
+
+def test_accept_matches_reference_fixture(golden_dir):
+    f = np.load(os.path.join(golden_dir, "accept.npz"))
+    for (T, k, p, seed), X, d, j, toks in zip(f["params"], f["x"], f["drafts"], f["j"], f["tokens"]):
+        got_j, got_t, st = orc.accept(orc.Rng(int(seed)), X, d, X.shape[1], T, int(k), p)
+        assert st == 0 and got_j == j
+        assert np.array_equal(got_t[:j + 1], toks[:j + 1])
+    assert sorted(set(f["j"].tolist())) == [0, 1, 2, 3, 4, 5]
+
+
+def test_accept_nan_row_fails():
+    X = np.random.default_rng(15).standard_normal((3, 64)).astype(np.float32)
+    X[0, 0] = np.nan
+    j, t, st = orc.accept(orc.Rng(1), X, np.array([1, 2], np.int32), 64, 0.7, 40, 0.95)
+    assert st == 1 and j == 0
+
+
+@pytest.mark.skipif(not orc.ref_available(), reason="oracle/_ref not built (needs the reference tree)")
+@pytest.mark.parametrize("T,k,p", [(0.7, 40, 0.95), (1.3, 64, 0.8), (0.9, 65, 0.99), (0.5, 0, 0.9), (2.0, 0, 1.0)])
+def test_sampler_matches_live_reference(T, k, p):
+    rng = np.random.default_rng(16)
+    X = (rng.standard_normal((40, 700)) * 2).astype(np.float32)
+    s = orc.RefSampler(T, k, p, 99, 700)
+    r = orc.Rng(99)
+    for row in X:
+        assert orc.sample_row(r, row, 700, T, k, p) == s.sample(row)
+
+
+def test_canonical_draw_is_libstdcxx_uniform():
+    # uniform_real_distribution<double>(0, b) = b * generate_canonical: the device acceptance kernel takes these
+    # draws from the host, so the host helper must be the exact same sequence.
+    r1, r2 = orc.Rng(5), orc.Rng(5)
+    X = np.zeros((1, 2), np.float32)  # two equal logits: draw u * 2 < 1 picks id 0
+    for _ in range(50):
+        u = r1.canonical()
+        assert orc.sample_row(r2, X[0], 2, 1.0, 0, 1.0) == (0 if u * 2.0 < 1.0 else 1)

@@ -1,0 +1,35 @@
+"""Shared helpers for the tests: seeded synthetic weights in the reference layout and bf16 bit conversions."""
+import numpy as np
+
+from oracle import oracle as orc
+
+
+def f32_to_bf16(a):
+    """Round-to-nearest-even FP32 -> BF16 bits (uint16), NaN kept quiet: formats/q4.cpp:12-19's conversion."""
+    a = np.ascontiguousarray(a, np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7F800000) == 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    keep = ((u >> np.uint64(16)) | np.where((u & 0x7FFFFF) != 0, np.uint64(0x40), np.uint64(0))) & 0xFFFF
+    return np.where(nan, keep, r).astype(np.uint16)
+
+
+def bf16_to_f32(b):
+    return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def rand_qweight(rng, bits, N, K, G):
+    """Uniform codes, scale = bf16(|N(0, 0.02)|), min = bf16(-(2^bits - 1) / 2 * scale): zero-mean weights."""
+    q = rng.integers(0, 256, N * K // (2 if bits == 4 else 1), dtype=np.uint8)
+    s = np.abs(rng.standard_normal(N * (K // G)) * 0.02).astype(np.float32)
+    sb = f32_to_bf16(s)
+    half = 7.5 if bits == 4 else 127.5
+    mb = f32_to_bf16(-half * bf16_to_f32(sb))
+    return orc.QWeight(bits, q, sb, mb, N, K, G)
+
+
+def max_abs_norm_err(got, ref):
+    """max |got - ref| / max |ref|: the north star's 1e-3 tolerance measure."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
