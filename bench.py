@@ -1,0 +1,243 @@
+"""Benchmark of strixite's MTP verify path on one MI355X (BASELINE.json's metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extra]
+
+A step is one MoE FFN verify sublayer: M = 6 tokens, hidden 4096, 512 experts, top-10 routing
+from FP32 router logits, SwiGLU experts (gate_up [1024 x 2 x 4096], down [4096 x 1024]) in q4 G = 128. Each step takes
+the next of 16 distinct token batches (different routing each, so the 3.4 GB of experts are not served from the
+256 MB Infinity Cache), with every input resident in HBM before the timed region. One JSON line goes to stdout:
+value = microseconds per layer; roofline = the grouped gate_up + SwiGLU kernel (the dominant one) timed with HIP events
+on its stream; cpu_baseline = the CPU oracle's same layer on this host's cores. --extra adds configs 1, 2 and 5.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "µs/layer for q4 MoE verify at M=6 + achieved HBM GB/s; prefill tok/s"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--extra", action="store_true", help="also time configs 1, 2 and 5")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def events():
+    import torch
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_launches(fn, n, warm=5):
+    """Average milliseconds of fn() over n back-to-back launches on torch's current stream (HIP events)."""
+    import torch
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    a, b = events()
+    a.record()
+    for i in range(n):
+        fn(i)
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def moe_layer_bench(args, out):
+    import numpy as np
+    import torch
+
+    from strixite_amd import kernels as kx
+    from strixite_amd import synthetic as syn
+    from strixite_amd.verify import MoeVerifyLayer
+
+    E, d, I, k, M, R = 512, 4096, 1024, 10, 6, 16
+    Wr = syn.router_weight(E, d, seed=11)
+    gu = syn.qweight(4, E * 2 * I, d, 128, seed=12)
+    dn = syn.qweight(4, E * d, I, 128, seed=13)
+    xs = [syn.activations(M, d, seed=100 + r) for r in range(R)]
+    layer = MoeVerifyLayer(Wr, gu, dn, E, k, M)
+
+    # routing + distinct experts of each batch (untimed)
+    per_expert = (gu.nbytes() + dn.nbytes()) // E
+    gu_per_expert = gu.nbytes() // E
+    Us, bytes_layer, routes = [], [], []
+    for r in range(R):
+        layer.forward(xs[r])
+        ids = layer.ids.clone()
+        ws, _ = kx.group_routes(ids, E)
+        routes.append((ids, layer.coef.clone(), ws))
+        U = int(torch.unique(ids).numel())
+        Us.append(U)
+        bytes_layer.append(U * per_expert + Wr.numel() * 4 + 2 * M * d * 2)
+    torch.cuda.synchronize()
+
+    # the timed steps: whole layers, rotating the batches
+    for i in range(args.warmup):
+        layer.forward(xs[i % R])
+    torch.cuda.synchronize()
+    a, b = events()
+    t0 = time.perf_counter()
+    a.record()
+    for i in range(args.steps):
+        layer.forward(xs[i % R])
+    b.record()
+    b.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = a.elapsed_time(b)
+    us_layer = ms_total * 1e3 / args.steps
+    mean_bytes = sum(bytes_layer[i % R] for i in range(args.steps)) / args.steps
+    out["value"] = round(us_layer, 3)
+    out["ms_per_step"] = round(ms_total / args.steps, 6)
+    out["layer_GBps"] = round(mean_bytes / (us_layer * 1e-6) / 1e9, 1)
+    out["layer_hbm_frac"] = round(out["layer_GBps"] / HBM_PEAK_GBS, 4)
+    out["distinct_experts_mean"] = round(sum(Us) / R, 2)
+    out["wall_s"] = round(wall, 3)
+
+    # dominant kernel alone: grouped gate_up + SwiGLU over the same rotating routes
+    h = torch.empty((M, k, I), dtype=torch.bfloat16, device="cuda")
+
+    def gate_up(i):
+        ids, coef, ws = routes[i % R]
+        kx.gather_grouped(xs[i % R], gu, E, ws, M, k, swiglu=True, y=h)
+
+    n = max(args.steps, 64)
+    ms = time_launches(gate_up, n)
+    gu_bytes = sum(Us[i % R] * gu_per_expert + M * d * 2 + M * k * I * 2 for i in range(n)) / n
+    achieved = gu_bytes / (ms * 1e-3) / 1e9
+    out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                       "kernel": "qmm_kernel SWIGLU (grouped gate_up + SwiGLU)", "avg_launch_us": round(ms * 1e3, 3),
+                       "algorithmic_bytes_per_launch": int(gu_bytes)}
+
+    # the down projection + combine, alone
+    hh = [torch.randn((M, k, I), device="cuda").to(torch.bfloat16) for _ in range(R)]
+    yb = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
+    part = torch.empty((M * k, d), dtype=torch.float32, device="cuda")
+
+    def down(i):
+        ids, coef, ws = routes[i % R]
+        kx.combine_grouped(hh[i % R], dn, E, ids, coef, ws, partial=part, y=yb)
+
+    ms_dn = time_launches(down, n)
+    dn_bytes = sum(Us[i % R] * (dn.nbytes() // E) for i in range(n)) / n
+    out["down_combine"] = {"avg_us": round(ms_dn * 1e3, 3), "GBps": round(dn_bytes / (ms_dn * 1e-3) / 1e9, 1)}
+    return layer, xs, routes
+
+
+def cpu_baseline(layer, xs, budget_s):
+    """The CPU oracle's same layer (router projection, top-k, SwiGLU experts, combine; FP64 accumulation) on this
+    host's cores, over as many of the token batches as fit the time budget."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as orc
+    from strixite_amd import synthetic as syn
+
+    E, k, d, I = layer.E, layer.k, layer.d, layer.I
+    Wr = layer.Wr.cpu().numpy()
+    threads = os.cpu_count() or 1
+    done, t_total = 0, 0.0
+    cache = {}
+    for r, x in enumerate(xs):
+        xh = x.view(torch.int16).cpu().numpy().view(np.uint16)
+        # weights the batch touches, copied to the host before the clock starts (they are resident in RAM on a host)
+        logits = orc.linear_f32w(xh, Wr)
+        ids, coef, _ = orc.moe_router(logits, E, k)
+        touched = np.unique(ids)
+        for e in touched:
+            if e not in cache:
+                cache[e] = (syn.host_rows(layer.gate_up, e * 2 * I, (e + 1) * 2 * I), syn.host_rows(layer.down, e * d, (e + 1) * d))
+        remap = {e: i for i, e in enumerate(touched)}
+        U = len(touched)
+        cat = lambda j, z: np.concatenate([cache[e][j][z] for e in touched])
+        hgu = orc.QWeight(4, cat(0, 0), cat(0, 1), cat(0, 2), U * 2 * I, d, 128)
+        hdn = orc.QWeight(4, cat(1, 0), cat(1, 1), cat(1, 2), U * d, I, 128)
+        t0 = time.perf_counter()
+        logits = orc.linear_f32w(xh, Wr, threads=threads)
+        ids, coef, _ = orc.moe_router(logits, E, k)
+        rid = np.vectorize(remap.get)(ids).astype(np.int32)
+        h, _ = orc.experts_gather(xh, hgu, U, rid, swiglu=True, threads=threads)
+        orc.experts_combine(h, hdn, U, rid, coef, threads=threads)
+        t_total += time.perf_counter() - t0
+        done += 1
+        if t_total >= budget_s:
+            break
+    return {"value": round(t_total / done * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": f"{done} of the {len(xs)} token batches (M = 6 each) through the CPU oracle's layer, "
+                      f"FP64 accumulation, {threads} threads"}
+
+
+def extra_configs(out):
+    import torch
+
+    from strixite_amd import kernels as kx
+    from strixite_amd import synthetic as syn
+    from strixite_amd.verify import VerifyTail
+
+    res = {}
+    # configs 1 and 2: dense q4 / q8 GEMV, 8 weight replicas rotated (> 256 MB Infinity Cache for config 2)
+    for name, bits, N, K, G, M, act in (("cfg1_q4_4096x4096_M1_f32", 4, 4096, 4096, 128, 1, torch.float32),
+                                        ("cfg2_q4_12288x4096_M6", 4, 12288, 4096, 128, 6, torch.bfloat16),
+                                        ("cfg2_q8_12288x4096_M6", 8, 12288, 4096, 64, 6, torch.bfloat16)):
+        reps = [syn.qweight(bits, N, K, G, seed=30 + i) for i in range(8 if N > 4096 else 32)]
+        x = syn.activations(M, K, seed=40, dtype=act)
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        ms = time_launches(lambda i: kx.linear(x, reps[i % len(reps)], out_act=0, y=y), 400)
+        nbytes = reps[0].nbytes() + x.numel() * x.element_size() + y.numel() * 4
+        res[name] = {"us": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del reps
+    # config 5: q8 LM head 151936 x 4096 at M = 6 -> top-40 -> sampled acceptance of 5 drafts
+    V, d = 151936, 4096
+    w = syn.qweight(8, V, d, 64, seed=50)
+    h = syn.activations(6, d, seed=51)
+    tail = VerifyTail(w, V, 40, 6)
+    drafts = torch.randint(0, V, (5,), dtype=torch.int32, device="cuda")
+    u = torch.rand(6, dtype=torch.float64, device="cuda")
+    ms = time_launches(lambda i: tail.forward(h, drafts, u, 0.7, 40, 0.95), 100)
+    ms_head = time_launches(lambda i: kx.linear(h, w, out_act=0, y=tail.logits[:6]), 100)
+    nb = w.nbytes() + h.numel() * 2 + 2 * 6 * V * 4
+    res["cfg5_verify_tail"] = {"us": round(ms * 1e3, 3), "lm_head_us": round(ms_head * 1e3, 3),
+                               "lm_head_GBps": round((w.nbytes() + 6 * V * 4) / (ms_head * 1e-3) / 1e9, 1),
+                               "GBps": round(nb / (ms * 1e-3) / 1e9, 1)}
+    out["configs"] = res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported (multi-GPU is a "
+                                   "design note only)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    import strixite_amd
+    strixite_amd.lib()  # fails loudly without the built library
+
+    out = {"metric": METRIC, "value": None, "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": None, "higher_is_better": False, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": "moe_verify_layer: BASELINE config 3 (M=6, d=4096, E=512, top-10, I=1024, q4 G=128, "
+                                  "fp32 router)", "global_batch": 6, "seq_len": 6, "parallelism": "single-gpu"}}
+    torch.cuda.synchronize()
+    layer, xs, routes = moe_layer_bench(args, out)
+    if args.extra:
+        extra_configs(out)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(layer, xs, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,151 @@
+/* strixite_amd: MI355X (gfx950, CDNA4, wave64) kernels for strixite's MTP verify path, behind a C ABI.
+ *
+ * Every entry point is asynchronous on the caller's HIP stream (passed as `sx_stream`, a hipStream_t) unless it says
+ * otherwise, takes plain device pointers and sizes, and returns SX_OK (0) or an error code; sx_last_error() returns the
+ * calling thread's message for the last failure. Preconditions are checked on the host before any launch (the
+ * reference's STRIX_CHECK set); data-dependent failures go to 3-word device error slots (first writer wins) and NaN
+ * outputs, as in the reference. Nothing here allocates device memory: callers pass workspaces sized by the
+ * *_workspace_bytes functions.
+ *
+ * Each declaration names the reference interface it replaces (file:line in TheBeaninator/strixite). The C++ shim that
+ * gives the reference's own kernels/ *.hpp signatures on top of these is strixite_amd/integration/strix_kernels_shim.cpp.
+ */
+#ifndef STRIXITE_AMD_H
+#define STRIXITE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *sx_stream; /* hipStream_t */
+
+enum sx_status { SX_OK = 0, SX_EINVAL = 1, SX_EHIP = 2, SX_EUNSUPPORTED = 3 };
+
+/* Activation dtype: strix::kernels::Act (kernels/norm.hpp:20), F32 or BF16 raw bits. */
+enum sx_act { SX_ACT_F32 = 0, SX_ACT_BF16 = 1 };
+
+/* strix::kernels::MoeMath (kernels/moe_grouped.hpp:35). On gfx950 all three run the MFMA path on exact codes with
+ * FP32 accumulation (F32 semantics: the tightest of the three); the value is accepted for API compatibility. */
+enum sx_moe_math { SX_MOE_F32 = 0, SX_MOE_WMMA_BF16 = 1, SX_MOE_WMMA_F16 = 2 };
+
+/* Q4DeviceView (runtime/q4_device.hpp:13-18) / Q8DeviceView (runtime/q8_device.hpp:12-17): non-owning device views of
+ * a [N, K] weight in the formats/q4.hpp:3-6 / q8.hpp:3-11 layout. q: N*K/2 (q4, low nibble = even k) or N*K (q8) bytes,
+ * 16-byte aligned; scale, minv: [N, K/G] BF16 bits; G in {32, 64, 128}; w = code * scale + min. */
+typedef struct sx_qview {
+    const uint8_t *q;
+    const uint16_t *scale;
+    const uint16_t *minv;
+    int64_t N, K, G;
+} sx_qview;
+
+const char *sx_last_error(void);
+const char *sx_version(void);
+
+/* ---- dense dequantizing GEMV/GEMM: y[M, N] = x[M, K] * deq(W)^T, FP32 accumulation, one rounding at the store ----
+ * kernels/linear_q4.hpp:26-30 and kernels/linear_q8.hpp:13-14. out_act == act, or BF16 x -> F32 y. */
+int sx_linear_q4(const void *x, const sx_qview *w, void *y, int64_t M, int act, int out_act, sx_stream stream);
+int sx_linear_q8(const void *x, const sx_qview *w, void *y, int64_t M, int act, int out_act, sx_stream stream);
+
+/* ---- per-slot MoE experts (decode / short verify), kernels/linear_q4.hpp:32-58 ----
+ * w: E experts stacked [E*N, K]; ids [M, A] int32 device. err: >= 3 zeroed uint32 (device).
+ *   gather:         y[m, a, :] = x[m, :] * W[ids[m, a]]^T                          (linear_q4.hpp:42-43)
+ *   gather_swiglu:  h[m, a, j] = silu(g) * u over rows [gate (I) | up (I)]          (linear_q4.hpp:55-56)
+ *   combine:        y[m, :] = sum_a coef[m, a] * (h[m, a, :] * W[ids[m, a]]^T)      (linear_q4.hpp:44-46) */
+int sx_linear_q4_experts_gather(const void *x, const sx_qview *w, int64_t E, const int32_t *ids, int64_t M, int64_t A,
+                                void *y, int act, uint32_t *err, sx_stream stream);
+int sx_linear_q4_experts_gather_swiglu(const void *x, const sx_qview *w, int64_t E, const int32_t *ids, int64_t M,
+                                       int64_t A, void *h, int act, uint32_t *err, sx_stream stream);
+int sx_linear_q4_experts_combine(const void *h, const sx_qview *w, int64_t E, const int32_t *ids, const float *coef,
+                                 int64_t M, int64_t A, void *y, int act, uint32_t *err, sx_stream stream);
+/* report_expert_error (kernels/linear_q4.hpp:61): the 3 words already on the host; SX_EINVAL + message if set. */
+int sx_report_expert_error(const uint32_t e[3], const char *what);
+
+/* ---- MoE router, kernels/moe_router.hpp:33-43 ----
+ * Top k of E logits per token (value desc, lower index on a tie), coef = softmax over the k (FP32); optional shared
+ * slot k with id shared_id and coef sigmoid(shared logit). Non-finite logit: ids -1, coef NaN, err {1, token, expert}.
+ * k in 1..min(E, 32); E in 1..1024. */
+int sx_moe_router(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t k, const void *shared_logit,
+                  int64_t shared_ld, int32_t shared_id, int32_t *ids, float *coef, int act, uint32_t *err,
+                  sx_stream stream);
+/* report_router_error (kernels/moe_router.hpp:43). */
+int sx_report_router_error(const uint32_t e[3], const char *what);
+/* moe_shared_add / moe_shared_add_inject (kernels/moe_router.hpp:53-63). */
+int sx_moe_shared_add(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,
+                      uint32_t gate_index, int act, uint32_t *err, sx_stream stream);
+int sx_moe_shared_add_inject(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,
+                             uint32_t gate_index, void *x, const float *w_in, int64_t H, int act, uint32_t *err,
+                             sx_stream stream);
+
+/* ---- grouped MoE experts (verify width and prefill), kernels/moe_grouped.hpp:42-62 ----
+ * moe_group_routes buckets the M*A slots by expert into ws (int32 layout of moe_grouped.hip:63-81: header [n_tiles,
+ * S, E, n_wtiles], offsets [E+2], slots [S], 16-slot tiles, 64-slot tiles); slot order within a bucket is unspecified
+ * and no output depends on it. Bad ids go to bucket E and set err {1, id, slot}. */
+int sx_moe_route_workspace_bytes(int64_t M, int64_t A, int64_t E, size_t *bytes);
+int sx_moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void *ws, size_t ws_bytes, uint32_t *err,
+                        sx_stream stream);
+/* y [M, A, N] (linear_q4_experts_gather_grouped, moe_grouped.hpp:53-55). */
+int sx_linear_q4_experts_gather_grouped(const void *x, const sx_qview *w, int64_t E, const void *ws, size_t ws_bytes,
+                                        int64_t M, int64_t A, void *y, int act, int math, sx_stream stream);
+/* y [M, N]; partial: M*A*N FP32 scratch (linear_q4_experts_combine_grouped, moe_grouped.hpp:60-62). */
+int sx_linear_q4_experts_combine_grouped(const void *h, const sx_qview *w, int64_t E, const int32_t *ids,
+                                         const float *coef, const void *ws, size_t ws_bytes, float *partial, int64_t M,
+                                         int64_t A, void *y, int act, int math, sx_stream stream);
+/* Grouped gather with the SwiGLU epilogue: h [M, A, N/2] = swiglu(gather_grouped(x)), bit-identical to
+ * sx_linear_q4_experts_gather_grouped followed by sx_swiglu. No single reference counterpart: it fuses the two calls
+ * runtime/qwen4exp.cpp:1154-1156 makes. */
+int sx_linear_q4_experts_gather_swiglu_grouped(const void *x, const sx_qview *w, int64_t E, const void *ws,
+                                               size_t ws_bytes, int64_t M, int64_t A, void *h, int act,
+                                               sx_stream stream);
+
+/* ---- SwiGLU, kernels/swiglu.hpp:21: gu [rows, 2I] -> h [rows, I]; BF16: h = bf16(bf16(silu(g)) * u). ---- */
+int sx_swiglu(const void *gu, void *h, int64_t rows, int64_t I, int act, sx_stream stream);
+
+/* ---- dense FP32-weight projection: y[M, N] (F32) = x[M, K] (act) * W[N, K]^T. The router logits of BASELINE
+ * configs 3/4 (fp32 Wr); plays the role kernels/linear.hpp linear_bf16w plays at runtime/qwen4exp.cpp:1132-1137. ---- */
+int sx_linear_f32w(const void *x, const float *W, int64_t N, int64_t K, float *y, int64_t M, int act,
+                   sx_stream stream);
+
+/* ---- logits top-k, kernels/logits_topk.hpp:26-46 ----
+ * Per row the best k (value desc, lower id on a tie; -0 ties +0) of ids [0, n_valid); NaN left out and flagged in
+ * nan[row]; optional allow mask [rows, mask_words]; padding (-inf, INT32_MAX). k in 1..64 (the reference: 20). */
+typedef struct sx_logit_cand {
+    float v;
+    int32_t id;
+} sx_logit_cand; /* LogitCand, kernels/logits_topk.hpp:29-33 */
+int sx_logits_topk_workspace_bytes(int64_t rows, int64_t n_valid, int64_t k, size_t *bytes);
+int sx_logits_topk(const float *logits, int64_t rows, int64_t ld, int64_t n_valid, int64_t k, sx_logit_cand *out,
+                   uint32_t *nan, void *workspace, size_t workspace_bytes, const uint32_t *mask, int64_t mask_words,
+                   sx_stream stream);
+
+/* ---- MTP draft pick, kernels/mtp_pick.hpp:20-33: top-2 + NaN flag + the forward's error words, one 64-byte block.
+ * emb_err points at the 8-byte EmbeddingError slot (kernels/embedding.hpp:26-28). ---- */
+typedef struct sx_mtp_pick_s {
+    int32_t best;
+    float best_v, second_v;
+    uint32_t nan;
+    uint32_t err[9];
+    uint32_t pad;
+    unsigned long long emb;
+} sx_mtp_pick_t;
+int sx_mtp_pick(const float *logits, int64_t n, const uint32_t *router_err, const uint32_t *expert_err,
+                const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out, sx_stream stream);
+
+/* ---- draft acceptance on the device: serve/engine.cpp:592-610 with Sampler semantics (serve/sampler.cpp:183-248) ----
+ * cands [k+1, kc] (from sx_logits_topk, value desc), nan [k+1], drafts [k] (device). Row j is sampled (greedy:
+ * candidate 0; else temperature -> top_k (<= kc) -> top_p -> draw r = u[j] * kept, u[j] a host draw of
+ * std::generate_canonical<double, 53> from the engine's mt19937_64, in order), accepting while the sample equals
+ * drafts[j]. Writes out[0] = j (0..k), out[1] = status (0, or 1 + the row whose sampling failed: NaN or non-finite top
+ * logit), out[2 .. 2+j] = the j+1 tokens committed (the accepted drafts, then row j's sample: the correction, or row
+ * k's when all were accepted). Draws consumed on the host side: 0 (greedy) or j+1 (j on failure). */
+int sx_mtp_accept(const sx_logit_cand *cands, const uint32_t *nan, int64_t kc, const int32_t *drafts, int64_t k,
+                  const double *u, double temperature, int64_t top_k, double top_p, int64_t n_valid, int32_t *out,
+                  sx_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRIXITE_AMD_H */

@@ -1,0 +1,6 @@
+// qmm mode GATHER: one instantiation unit of qmm_impl.hpp.
+#include "qmm_impl.hpp"
+
+namespace sx::qmm::detail {
+template hipError_t launch_mode<GATHER>(int, int, int, const Params &, dim3, hipStream_t);
+}

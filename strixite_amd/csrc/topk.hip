@@ -1,0 +1,395 @@
+// The verify tail on gfx950: logits top-k (kernels/logits_topk.hpp:3-46), the MTP draft pick (kernels/mtp_pick.hpp:3-33)
+// and draft acceptance on the device (serve/engine.cpp:592-610 with serve/sampler.cpp:183-248's draw).
+#include "common.hpp"
+
+#include <climits>
+
+namespace sx {
+namespace {
+
+// ---------------- 64-bit candidate keys ----------------
+// A candidate (value, id) as one key whose unsigned order is the candidates' order: value bits made monotone in the
+// high word (-0 folded onto +0, so they tie as a float compare does), the id inverted in the low word (lower id
+// first). 0 = no candidate (no real candidate maps there: only a NaN bit pattern would, and NaNs are left out).
+__device__ __forceinline__ uint64_t cand_key(float v, int32_t id) {
+    const uint32_t b = v == 0.f ? 0u : __float_as_uint(v);
+    const uint32_t hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)hi << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)id);
+}
+__device__ __forceinline__ int32_t key_id(uint64_t k) { return (int32_t)(0xFFFFFFFFu - (uint32_t)k); }
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, int src) {
+    const uint32_t lo = __shfl((uint32_t)v, src), hi = __shfl((uint32_t)(v >> 32), src);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t umax(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t umin(uint64_t a, uint64_t b) { return a < b ? a : b; }
+
+// Bitonic sort of one key a lane across the wave, descending by lane (lane 0 = best): 21 compare-exchange stages.
+__device__ uint64_t wave_sort_desc(uint64_t v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint64_t o = shfl_xor64(v, stride);
+            const bool desc = (lane & size) == 0, lower = (lane & stride) == 0;
+            v = (lower == desc) ? umax(v, o) : umin(v, o);
+        }
+    return v;
+}
+
+// Top 64 of two descending lane-sorted lists: max against the other list reversed is bitonic, then 6 merge stages.
+__device__ uint64_t wave_merge_desc(uint64_t a, uint64_t b) {
+    const int lane = threadIdx.x & 63;
+    uint64_t c = umax(a, shfl64(b, 63 - lane));
+#pragma unroll
+    for (int stride = 32; stride > 0; stride >>= 1) {
+        const uint64_t o = shfl_xor64(c, stride);
+        c = (lane & stride) == 0 ? umax(c, o) : umin(c, o);
+    }
+    return c;
+}
+
+// The wave's best k (k <= 64) of the keys its lanes hold (P a lane), lane-sorted descending; lanes >= k hold 0.
+// Threshold: the k-th best lane maximum - at least k keys reach it, so every key of the top k does. The keys that
+// reach it (usually ~k: mostly the lane maxima) are compacted through LDS and sorted with one or a few bitonic passes.
+template <int P>
+__device__ uint64_t wave_topk(const uint64_t (&key)[P], int k, uint64_t *scratch, int scratch_cap) {
+    const int lane = threadIdx.x & 63;
+    uint64_t head = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) head = umax(head, key[p]);
+    const uint64_t tau = shfl64(wave_sort_desc(head), k - 1);  // 0 if fewer than k lanes hold anything
+    int cnt = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) cnt += (key[p] != 0 && key[p] >= tau) ? 1 : 0;
+    int incl = cnt;  // inclusive prefix of the counts across lanes
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+    }
+    const int total = __shfl(incl, 63);
+    uint64_t list = 0;
+    if (total <= scratch_cap) {
+        int at = incl - cnt;
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+            if (key[p] != 0 && key[p] >= tau) scratch[at++] = key[p];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        for (int b0 = 0; b0 < total; b0 += 64) {
+            const uint64_t c = b0 + lane < total ? scratch[b0 + lane] : 0;
+            const uint64_t s = wave_sort_desc(c);
+            list = b0 == 0 ? s : wave_merge_desc(list, s);
+        }
+        __builtin_amdgcn_wave_barrier();
+    } else {  // many keys at the threshold (heavy ties): merge column by column
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const uint64_t c = (key[p] != 0 && key[p] >= tau) ? key[p] : 0;
+            if (__ballot(c != 0) == 0) continue;
+            list = wave_merge_desc(list, wave_sort_desc(c));
+        }
+    }
+    return lane < k ? list : 0;
+}
+
+// ---------------- logits top-k ----------------
+// One level: workgroup g of row r reduces up to kGroup inputs - logits (level 1: ids = positions < n_valid, NaN
+// flagged and left out, masked ids left out) or an earlier level's key lists - to its best k keys. Each wave takes a
+// strided quarter (coalesced loads), finds its best k (wave_topk), and wave 0 merges the four lists.
+constexpr int kTopkThreads = 256;
+constexpr int kPer = 32;                      // inputs a thread holds
+constexpr int kGroup = kTopkThreads * kPer;   // inputs a workgroup reduces
+constexpr int kScratch = 256;                 // compaction room a wave (keys)
+
+template <bool kLogits, bool kMasked>
+__global__ void __launch_bounds__(kTopkThreads)
+    topk_level_kernel(const float *logits, int64_t ld, int n_valid, const uint64_t *in, int n_in, int groups, int k,
+                      uint64_t *out_keys, sx_logit_cand *out_final, uint32_t *nan_level1, int groups1, uint32_t *nan,
+                      const uint32_t *mask, int64_t mask_words) {
+    __shared__ uint64_t scratch[kTopkThreads / 64][kScratch];
+    __shared__ uint64_t lists[kTopkThreads / 64][64];
+    __shared__ uint32_t s_nan;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = blockIdx.x;
+    const int64_t r = blockIdx.y;
+    if (t == 0) s_nan = 0;
+    uint64_t key[kPer];
+    uint32_t my_nan = 0;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+        const int j = g * kGroup + p * kTopkThreads + t;
+        key[p] = 0;
+        if constexpr (kLogits) {
+            if (j < n_valid) {
+                const float x = logits[r * ld + j];
+                const bool allowed = !kMasked || ((mask[r * mask_words + (j >> 5)] >> (j & 31)) & 1u);
+                if (x != x) my_nan = 1u;  // flagged whether the id is allowed or not
+                else if (allowed) key[p] = cand_key(x, j);
+            }
+        } else if (j < n_in) {
+            key[p] = in[r * n_in + j];
+        }
+    }
+    __syncthreads();
+    if (my_nan) atomicOr(&s_nan, 1u);
+    const uint64_t mine = wave_topk<kPer>(key, k, scratch[wave], kScratch);
+    lists[wave][lane] = mine;
+    __syncthreads();
+    if (wave != 0) return;
+    uint64_t best = lists[0][lane];
+#pragma unroll
+    for (int w = 1; w < kTopkThreads / 64; ++w) {
+        best = wave_merge_desc(best, lists[w][lane]);
+        best = lane < k ? best : 0;
+    }
+    if (groups > 1) {
+        if (lane < k) out_keys[(r * groups + g) * k + lane] = best;
+    } else if (lane < k) {  // the last level: candidates with their values read back from the row (keeps -0)
+        sx_logit_cand c;
+        if (best == 0) c.v = -INFINITY, c.id = INT32_MAX;
+        else c.id = key_id(best), c.v = logits[r * ld + c.id];
+        out_final[r * k + lane] = c;
+    }
+    if (lane == 0) {
+        if constexpr (kLogits) {
+            nan_level1[r * groups + g] = s_nan;
+            if (groups == 1) nan[r] = s_nan;
+        } else if (groups == 1) {
+            uint32_t f = 0;
+            for (int c = 0; c < groups1; ++c) f |= nan_level1[r * groups1 + c];
+            nan[r] = f;
+        }
+    }
+}
+
+int64_t groups_of(int64_t n) { return (n + kGroup - 1) / kGroup; }
+
+// ---------------- MTP draft pick ----------------
+constexpr int kPickThreads = 1024;
+
+struct Top2 {
+    float b1, b2;
+    int i1;  // INT_MAX: nothing seen
+    uint32_t nan;
+};
+
+__device__ __forceinline__ Top2 top2_merge(const Top2 &a, const Top2 &b) {
+    if (b.i1 == INT_MAX) return {a.b1, a.b2, a.i1, a.nan | b.nan};
+    if (a.i1 == INT_MAX) return {b.b1, b.b2, b.i1, a.nan | b.nan};
+    const bool a_wins = a.b1 > b.b1 || (a.b1 == b.b1 && a.i1 < b.i1);
+    const Top2 &w = a_wins ? a : b, &l = a_wins ? b : a;
+    return {w.b1, fmaxf(w.b2, l.b1), w.i1, a.nan | b.nan};  // the loser's best is at least its own runner-up
+}
+
+__device__ __forceinline__ Top2 top2_xor(const Top2 &p, int off) {
+    return {__shfl_xor(p.b1, off), __shfl_xor(p.b2, off), __shfl_xor(p.i1, off),
+            (uint32_t)__shfl_xor((int)p.nan, off)};
+}
+
+__global__ void __launch_bounds__(kPickThreads)
+    mtp_pick_kernel(const float *x, int64_t n, const uint32_t *router_err, const uint32_t *expert_err,
+                    const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out) {
+    __shared__ Top2 part[kPickThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    Top2 p{-INFINITY, -INFINITY, INT_MAX, 0u};
+    // A thread's indices ascend, so the strict > keeps the lower index of equal values.
+    for (int64_t i = tid; i < n; i += kPickThreads) {
+        const float v = x[i];
+        if (v != v) {
+            p.nan = 1u;
+            continue;
+        }
+        if (p.i1 == INT_MAX || v > p.b1) p.b2 = p.b1, p.b1 = v, p.i1 = (int)i;
+        else if (v > p.b2) p.b2 = v;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) p = top2_merge(p, top2_xor(p, off));
+    if (lane == 0) part[wave] = p;
+    __syncthreads();
+    if (wave != 0) return;
+    p = lane < kPickThreads / 64 ? part[lane] : Top2{-INFINITY, -INFINITY, INT_MAX, 0u};
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) p = top2_merge(p, top2_xor(p, off));
+    if (lane == 0) {
+        out->best = p.i1 == INT_MAX ? 0 : p.i1;  // every logit NaN: 0, flagged
+        out->best_v = p.b1, out->second_v = p.b2, out->nan = p.nan;
+        out->pad = 0;
+        out->emb = *emb_err;
+    }
+    if (lane < 3) {
+        out->err[lane] = router_err[lane];
+        out->err[3 + lane] = expert_err[lane];
+        out->err[6 + lane] = attn_err[lane];
+    }
+}
+
+// ---------------- draft acceptance ----------------
+// One lane walks the rows in order, exactly as the engine's loop and the sampler's draw do on the host: the sums are
+// sequential in double, the draw r = u * kept with u the host's generate_canonical<double, 53> for that row.
+__global__ void __launch_bounds__(64)
+    mtp_accept_kernel(const sx_logit_cand *cands, const uint32_t *nan, int kc, const int32_t *drafts, int k,
+                      const double *u, double temperature, int top_k, double top_p, int64_t n_valid, int32_t *out) {
+    if (threadIdx.x != 0) return;
+    int status = 0, j = 0;
+    for (;; ++j) {
+        const sx_logit_cand *c = cands + (int64_t)j * kc;
+        int32_t v = -1;
+        bool ok = nan[j] == 0;
+        // serve/sampler.cpp:192-201: real candidates (ids in range) first, then only padding; at least one real.
+        bool padding = false;
+        const int m = kc < 20 ? kc : 20;
+        for (int i = 0; ok && i < m; ++i) {
+            const bool pad = c[i].id == INT32_MAX && c[i].v == -INFINITY;
+            ok = pad || (!padding && c[i].id >= 0 && c[i].id < n_valid);
+            padding |= pad;
+        }
+        ok = ok && c[0].id != INT32_MAX;
+        if (ok && temperature == 0) {
+            v = c[0].id;
+        } else if (ok) {
+            const int kk = (int)(top_k < n_valid ? top_k : n_valid);
+            ok = isfinite(c[0].v);
+            if (ok) {
+                // prob_i recomputed where used (the same double exp each time): no per-lane array in scratch.
+                const double top = (double)c[0].v / temperature;
+                auto prob = [&](int i) { return exp((double)c[i].v / temperature - top); };
+                double sum = 0;
+                for (int i = 0; i < kk; ++i) sum += prob(i);
+                int keep = kk;
+                if (top_p < 1) {
+                    double acc = 0;
+                    for (int i = 0; i < kk; ++i) {
+                        acc += prob(i) / sum;
+                        if (acc >= top_p) {
+                            keep = i + 1;
+                            break;
+                        }
+                    }
+                }
+                double kept = 0;
+                for (int i = 0; i < keep; ++i) kept += prob(i);
+                const double r = u[j] * kept;
+                double acc = 0;
+                v = c[keep - 1].id;
+                for (int i = 0; i < keep; ++i) {
+                    acc += prob(i);
+                    if (r < acc) {
+                        v = c[i].id;
+                        break;
+                    }
+                }
+            }
+        }
+        if (!ok) {
+            status = 1 + j;
+            break;
+        }
+        out[2 + j] = v;
+        if (j == k || v != drafts[j]) break;
+    }
+    out[0] = j;
+    out[1] = status;
+}
+
+}  // namespace
+}  // namespace sx
+
+using namespace sx;
+
+extern "C" {
+
+int sx_logits_topk_workspace_bytes(int64_t rows, int64_t n_valid, int64_t k, size_t *bytes) {
+    SX_CHECK(bytes != nullptr, "null output");
+    SX_CHECK(rows >= 1 && n_valid >= 1 && n_valid <= (1 << 24) && k >= 1 && k <= 64, "rows = ", rows, ", n_valid = ",
+             n_valid, ", k = ", k, " (expected rows >= 1, n_valid 1..2^24, k 1..64)");
+    const int64_t g1 = groups_of(n_valid);
+    *bytes = 2 * (size_t)(rows * g1 * k) * 8 + (size_t)(rows * g1) * 4;
+    return SX_OK;
+}
+
+int sx_logits_topk(const float *logits, int64_t rows, int64_t ld, int64_t n_valid, int64_t k, sx_logit_cand *out,
+                   uint32_t *nan, void *workspace, size_t workspace_bytes, const uint32_t *mask, int64_t mask_words,
+                   sx_stream stream) {
+    SX_CHECK(logits && out && nan && workspace, "null pointer (logits=", (const void *)logits, ", out=", (void *)out,
+             ", nan=", (void *)nan, ", workspace=", workspace, ")");
+    SX_CHECK(rows >= 1 && rows <= 65535, "rows = ", rows, ", expected 1..65535");
+    SX_CHECK(n_valid >= 1 && n_valid <= (1 << 24), "n_valid = ", n_valid, ", expected 1..2^24");
+    SX_CHECK(k >= 1 && k <= 64, "k = ", k, ", expected 1..64");
+    SX_CHECK(ld >= n_valid, "row stride ld = ", ld, " < n_valid = ", n_valid);
+    size_t need = 0;
+    if (int rc = sx_logits_topk_workspace_bytes(rows, n_valid, k, &need)) return rc;
+    SX_CHECK(workspace_bytes >= need, "workspace ", workspace_bytes, " bytes, need ", need, " for ", rows, " rows of ",
+             n_valid);
+    SX_CHECK(aligned(workspace, 8), "workspace must be 8-byte aligned");
+    if (mask != nullptr) {
+        SX_CHECK(mask_words >= (n_valid + 31) / 32, "mask_words = ", mask_words, " per row covers ", mask_words * 32,
+                 " ids, need ", (n_valid + 31) / 32, " words for n_valid = ", n_valid);
+        SX_CHECK(aligned(mask, 4), "mask must be 4-byte aligned");
+    } else {
+        SX_CHECK(mask_words == 0, "mask_words = ", mask_words, " without a mask (pass 0 when mask is null)");
+    }
+    hipStream_t s = stream_of(stream);
+    const int64_t g1 = groups_of(n_valid);
+    auto *buf0 = static_cast<uint64_t *>(workspace);
+    uint64_t *buf1 = buf0 + rows * g1 * k;
+    auto *nan1 = reinterpret_cast<uint32_t *>(buf1 + rows * g1 * k);
+    const dim3 grid1((unsigned)g1, (unsigned)rows);
+    if (mask != nullptr)
+        topk_level_kernel<true, true><<<grid1, kTopkThreads, 0, s>>>(logits, ld, (int)n_valid, nullptr, 0, (int)g1,
+                                                                      (int)k, buf0, out, nan1, (int)g1, nan, mask,
+                                                                      mask_words);
+    else
+        topk_level_kernel<true, false><<<grid1, kTopkThreads, 0, s>>>(logits, ld, (int)n_valid, nullptr, 0, (int)g1,
+                                                                       (int)k, buf0, out, nan1, (int)g1, nan, nullptr, 0);
+    SX_LAUNCHED("logits_topk level 1 rows=", rows, " n_valid=", n_valid);
+    uint64_t *cur = buf0;
+    for (int64_t groups = g1, level = 2; groups > 1; ++level) {
+        const int64_t n_in = groups * k, next = groups_of(n_in);
+        uint64_t *dst = cur == buf0 ? buf1 : buf0;
+        topk_level_kernel<false, false><<<dim3((unsigned)next, (unsigned)rows), kTopkThreads, 0, s>>>(
+            logits, ld, 0, cur, (int)n_in, (int)next, (int)k, dst, out, nan1, (int)g1, nan, nullptr, 0);
+        SX_LAUNCHED("logits_topk level ", level, " rows=", rows, " candidates=", n_in);
+        cur = dst, groups = next;
+    }
+    return SX_OK;
+}
+
+int sx_mtp_pick(const float *logits, int64_t n, const uint32_t *router_err, const uint32_t *expert_err,
+                const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out, sx_stream stream) {
+    SX_CHECK(logits && router_err && expert_err && attn_err && emb_err && out, "null pointer");
+    SX_CHECK(n >= 1 && n <= INT_MAX, "n = ", n, " logits, expected 1..", INT_MAX);
+    mtp_pick_kernel<<<1, kPickThreads, 0, stream_of(stream)>>>(logits, n, router_err, expert_err, attn_err, emb_err,
+                                                              out);
+    SX_LAUNCHED("mtp_pick n=", n);
+    return SX_OK;
+}
+
+int sx_mtp_accept(const sx_logit_cand *cands, const uint32_t *nan, int64_t kc, const int32_t *drafts, int64_t k,
+                  const double *u, double temperature, int64_t top_k, double top_p, int64_t n_valid, int32_t *out,
+                  sx_stream stream) {
+    SX_CHECK(cands && nan && out && (k == 0 || drafts), "null pointer");
+    SX_CHECK(k >= 0 && k <= 15, "k = ", k, " drafts, expected 0..15 (mtp-draft's range)");
+    SX_CHECK(kc >= 1 && kc <= 64, "kc = ", kc, " candidates a row, expected 1..64");
+    SX_CHECK(n_valid >= 1, "n_valid = ", n_valid);
+    SX_CHECK(temperature >= 0 && temperature <= 100, "temperature ", temperature, ", expected 0..100");
+    SX_CHECK(top_p > 0 && top_p <= 1, "top_p ", top_p, ", expected (0, 1]");
+    SX_CHECK(kc >= (n_valid < 20 ? n_valid : 20), "kc = ", kc, " candidates, the sampler needs min(n_valid, 20)");
+    if (temperature > 0) {
+        SX_CHECK(u != nullptr, "sampled acceptance needs the host's uniform draws");
+        SX_CHECK(top_k >= 1 && top_k <= kc, "top_k = ", top_k, " must be 1..", kc,
+                 " (the candidates a row; top_k off needs the whole row)");
+    }
+    mtp_accept_kernel<<<1, 64, 0, stream_of(stream)>>>(cands, nan, (int)kc, drafts, (int)k, u, temperature,
+                                                       (int)top_k, top_p, n_valid, out);
+    SX_LAUNCHED("mtp_accept k=", k);
+    return SX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,204 @@
+"""Python face of the C ABI over torch device tensors: the reference's strix::kernels operators by name
+(kernels/linear_q4.hpp, linear_q8.hpp, moe_router.hpp, moe_grouped.hpp, swiglu.hpp, logits_topk.hpp, mtp_pick.hpp).
+
+torch supplies device memory and the stream (torch.cuda.current_stream() unless one is passed); every computation is
+a libstrixite_amd.so kernel. Activations are torch.float32 (Act::F32) or torch.bfloat16 (Act::BF16, raw bits).
+"""
+import ctypes
+
+import torch
+
+from . import (ACT_BF16, ACT_F32, MOE_F32, LogitCand, MtpPick, QView, check, lib)
+
+_c = ctypes.c_void_p
+
+
+def _p(t):
+    return None if t is None else _c(t.data_ptr())
+
+
+def _s(stream=None):
+    return _c((stream if stream is not None else torch.cuda.current_stream()).cuda_stream)
+
+
+def act_of(t):
+    if t.dtype == torch.float32:
+        return ACT_F32
+    if t.dtype == torch.bfloat16:
+        return ACT_BF16
+    raise TypeError(f"activations are float32 or bfloat16, got {t.dtype}")
+
+
+def dtype_of(act):
+    return torch.float32 if act == ACT_F32 else torch.bfloat16
+
+
+class QWeight:
+    """A q4 / q8 weight resident on the device (Q4Device / Q8Device, runtime/q4_device.hpp:23-36): codes uint8,
+    scale / min as BF16 bits (int16 tensors), in the formats/q4.hpp / q8.hpp layout."""
+
+    def __init__(self, bits, q, scale, minv, N, K, G):
+        self.bits, self.q, self.scale, self.minv = bits, q, scale, minv
+        self.N, self.K, self.G = int(N), int(K), int(G)
+        self._view = QView(q.data_ptr(), scale.data_ptr(), minv.data_ptr(), self.N, self.K, self.G)
+
+    @classmethod
+    def upload(cls, host, device="cuda"):
+        """From a host weight with numpy arrays q, scale, minv (e.g. oracle.QWeight)."""
+        t = lambda a: torch.from_numpy(a.view(a.dtype)).to(device)
+        return cls(host.bits, t(host.q), t(host.scale.view("int16")), t(host.minv.view("int16")), host.N, host.K, host.G)
+
+    def view(self):
+        return ctypes.byref(self._view)
+
+    def nbytes(self):
+        return self.q.numel() + 2 * self.scale.numel() + 2 * self.minv.numel()
+
+
+def linear(x, w, out_act=None, y=None, stream=None):
+    """y[M, N] = x[M, K] * deq(W)^T (linear_q4 / linear_q8)."""
+    act = act_of(x)
+    out_act = act if out_act is None else out_act
+    M = x.shape[0]
+    if y is None:
+        y = torch.empty((M, w.N), dtype=dtype_of(out_act), device=x.device)
+    f = lib().sx_linear_q4 if w.bits == 4 else lib().sx_linear_q8
+    check(f(_p(x), w.view(), _p(y), M, act, out_act, _s(stream)))
+    return y
+
+
+def _err(device):
+    return torch.zeros(4, dtype=torch.int32, device=device)
+
+
+def experts_gather(x, w, E, ids, swiglu=False, y=None, err=None, stream=None):
+    """Per-slot gather (linear_q4_experts_gather) or its SwiGLU form (linear_q4_experts_gather_swiglu)."""
+    act = act_of(x)
+    M, A = ids.shape
+    N = w.N // E
+    out_n = N // 2 if swiglu else N
+    y = torch.empty((M, A, out_n), dtype=x.dtype, device=x.device) if y is None else y
+    err = _err(x.device) if err is None else err
+    f = lib().sx_linear_q4_experts_gather_swiglu if swiglu else lib().sx_linear_q4_experts_gather
+    check(f(_p(x), w.view(), E, _p(ids), M, A, _p(y), act, _p(err), _s(stream)))
+    return y, err
+
+
+def experts_combine(h, w, E, ids, coef, y=None, err=None, stream=None):
+    act = act_of(h)
+    M, A = ids.shape
+    N = w.N // E
+    y = torch.empty((M, N), dtype=h.dtype, device=h.device) if y is None else y
+    err = _err(h.device) if err is None else err
+    check(lib().sx_linear_q4_experts_combine(_p(h), w.view(), E, _p(ids), _p(coef), M, A, _p(y), act, _p(err),
+                                             _s(stream)))
+    return y, err
+
+
+def moe_router(logits, E, k, shared=None, shared_ld=1, shared_id=0, ids=None, coef=None, err=None, stream=None):
+    M, ld = logits.shape
+    A = k + (1 if shared is not None else 0)
+    ids = torch.empty((M, A), dtype=torch.int32, device=logits.device) if ids is None else ids
+    coef = torch.empty((M, A), dtype=torch.float32, device=logits.device) if coef is None else coef
+    err = _err(logits.device) if err is None else err
+    check(lib().sx_moe_router(_p(logits), ld, M, E, k, _p(shared), shared_ld, shared_id, _p(ids), _p(coef),
+                              act_of(logits), _p(err), _s(stream)))
+    return ids, coef, err
+
+
+def route_workspace_bytes(M, A, E):
+    n = ctypes.c_size_t()
+    check(lib().sx_moe_route_workspace_bytes(M, A, E, ctypes.byref(n)))
+    return n.value
+
+
+def group_routes(ids, E, ws=None, err=None, stream=None):
+    M, A = ids.shape
+    nb = route_workspace_bytes(M, A, E)
+    ws = torch.empty(nb // 4, dtype=torch.int32, device=ids.device) if ws is None else ws
+    err = _err(ids.device) if err is None else err
+    check(lib().sx_moe_group_routes(_p(ids), M, A, E, _p(ws), ws.numel() * 4, _p(err), _s(stream)))
+    return ws, err
+
+
+def gather_grouped(x, w, E, ws, M, A, swiglu=False, y=None, math=MOE_F32, stream=None):
+    act = act_of(x)
+    N = w.N // E
+    out_n = N // 2 if swiglu else N
+    y = torch.empty((M, A, out_n), dtype=x.dtype, device=x.device) if y is None else y
+    if swiglu:
+        check(lib().sx_linear_q4_experts_gather_swiglu_grouped(_p(x), w.view(), E, _p(ws), ws.numel() * 4, M, A, _p(y),
+                                                               act, _s(stream)))
+    else:
+        check(lib().sx_linear_q4_experts_gather_grouped(_p(x), w.view(), E, _p(ws), ws.numel() * 4, M, A, _p(y), act,
+                                                        math, _s(stream)))
+    return y
+
+
+def combine_grouped(h, w, E, ids, coef, ws, partial=None, y=None, math=MOE_F32, stream=None):
+    act = act_of(h)
+    M, A = ids.shape
+    N = w.N // E
+    y = torch.empty((M, N), dtype=h.dtype, device=h.device) if y is None else y
+    partial = torch.empty((M * A, N), dtype=torch.float32, device=h.device) if partial is None else partial
+    check(lib().sx_linear_q4_experts_combine_grouped(_p(h), w.view(), E, _p(ids), _p(coef), _p(ws), ws.numel() * 4,
+                                                     _p(partial), M, A, _p(y), act, math, _s(stream)))
+    return y
+
+
+def swiglu(gu, h=None, stream=None):
+    rows, I2 = gu.shape
+    h = torch.empty((rows, I2 // 2), dtype=gu.dtype, device=gu.device) if h is None else h
+    check(lib().sx_swiglu(_p(gu), _p(h), rows, I2 // 2, act_of(gu), _s(stream)))
+    return h
+
+
+def linear_f32w(x, W, y=None, stream=None):
+    M, K = x.shape
+    N = W.shape[0]
+    y = torch.empty((M, N), dtype=torch.float32, device=x.device) if y is None else y
+    check(lib().sx_linear_f32w(_p(x), _p(W), N, K, _p(y), M, act_of(x), _s(stream)))
+    return y
+
+
+def topk_workspace_bytes(rows, n_valid, k):
+    n = ctypes.c_size_t()
+    check(lib().sx_logits_topk_workspace_bytes(rows, n_valid, k, ctypes.byref(n)))
+    return n.value
+
+
+def logits_topk(logits, n_valid, k=20, mask=None, ws=None, out=None, nan=None, stream=None):
+    """Per row the best k (value desc, lower id on a tie). Returns (values f32 [rows, k], ids i32 [rows, k], nan)."""
+    rows, ld = logits.shape
+    out = torch.empty((rows, k, 2), dtype=torch.int32, device=logits.device) if out is None else out
+    nan = torch.empty(rows, dtype=torch.int32, device=logits.device) if nan is None else nan
+    if ws is None:
+        ws = torch.empty(topk_workspace_bytes(rows, n_valid, k) // 8 + 1, dtype=torch.int64, device=logits.device)
+    mw = 0 if mask is None else mask.shape[1]
+    check(lib().sx_logits_topk(_p(logits), rows, ld, n_valid, k, _p(out), _p(nan), _p(ws), ws.numel() * 8, _p(mask), mw,
+                               _s(stream)))
+    return out[..., 0].view(torch.float32), out[..., 1], nan, out
+
+
+def mtp_pick(logits, router_err, expert_err, attn_err, emb_err, out=None, stream=None):
+    out = torch.empty(64, dtype=torch.uint8, device=logits.device) if out is None else out
+    check(lib().sx_mtp_pick(_p(logits), logits.numel(), _p(router_err), _p(expert_err), _p(attn_err), _p(emb_err),
+                            _p(out), _s(stream)))
+    return out
+
+
+def pick_from_bytes(b):
+    """The 64 bytes of an sx_mtp_pick_t (host) as the ctypes struct."""
+    return MtpPick.from_buffer_copy(bytes(b.cpu().numpy().tobytes()))
+
+
+def mtp_accept(cands, nan, drafts, u, temperature, top_k, top_p, n_valid, out=None, stream=None):
+    """cands: the raw [k+1, kc, 2] int32 output of logits_topk. Returns the device int32 vector
+    [j, status, tokens...]."""
+    rows, kc = cands.shape[0], cands.shape[1]
+    k = drafts.numel()
+    assert rows >= k + 1, "one candidate row per draft plus the last"
+    out = torch.full((2 + k + 1,), -1, dtype=torch.int32, device=cands.device) if out is None else out
+    check(lib().sx_mtp_accept(_p(cands), _p(nan), kc, _p(drafts), k, _p(u), float(temperature), int(top_k),
+                              float(top_p), int(n_valid), _p(out), _s(stream)))
+    return out

@@ -1,0 +1,74 @@
+"""The C-ABI library without a GPU: it loads, exports every symbol include/strixite_amd.h declares, and its host-side
+precondition checks answer before any launch (CPU only)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import strixite_amd as sx
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "strixite_amd.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(sx.LIB_PATH):
+        from strixite_amd import build
+        build.build(verbose=False)
+    return sx.lib()
+
+
+def declared():
+    text = open(HEADER).read()
+    return set(re.findall(r"^\s*(?:int|const char \*)\s*(sx_\w+)\s*\(", text, re.M))
+
+
+def test_header_and_python_signatures_agree():
+    assert declared() == set(sx.SIGNATURES), declared() ^ set(sx.SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(L):
+    for name in declared():
+        assert hasattr(L, name), name
+    assert b"gfx950" in L.sx_version()
+
+
+def test_precondition_errors_name_the_problem(L):
+    w = sx.QView(None, None, None, 16, 128, 128)
+    rc = L.sx_linear_q4(None, ctypes.byref(w), None, 1, sx.ACT_BF16, sx.ACT_BF16, None)
+    assert rc == sx.SX_EINVAL and b"null pointer" in L.sx_last_error()
+    # a weight view with a bad group size (kernels/linear_q4.hip:418)
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p).value
+    w = sx.QView(p, p, p, 16, 128, 48)
+    rc = L.sx_linear_q8(ctypes.c_void_p(p), ctypes.byref(w), ctypes.c_void_p(p + 32), 1, sx.ACT_BF16, sx.ACT_BF16, None)
+    assert rc == sx.SX_EINVAL and b"group size 48" in L.sx_last_error()
+    # k above the router's 32 (kernels/moe_router.hpp:37)
+    rc = L.sx_moe_router(ctypes.c_void_p(p), 512, 1, 512, 33, None, 0, 0, ctypes.c_void_p(p), ctypes.c_void_p(p + 8),
+                         sx.ACT_F32, ctypes.c_void_p(p + 16), None)
+    assert rc == sx.SX_EINVAL and b"k = 33" in L.sx_last_error()
+
+
+def test_route_workspace_layout_contract(L):
+    # kernels/moe_grouped.hip:63-81: [4 header] [E + 2 offsets] [S slots] [2 x Tmax] [2 x WTmax], Tmax = S/16 + E + 2,
+    # WTmax = S/64 + E + 2.
+    for M, A, E in [(6, 10, 512), (2048, 10, 512), (1, 1, 1), (3, 11, 513)]:
+        S = M * A
+        n = ctypes.c_size_t()
+        assert L.sx_moe_route_workspace_bytes(M, A, E, ctypes.byref(n)) == 0
+        assert n.value == 4 * (4 + E + 2 + S + 2 * (S // 16 + E + 2) + 2 * (S // 64 + E + 2))
+    assert L.sx_moe_route_workspace_bytes(1, 1, 1024, ctypes.byref(n)) == sx.SX_EINVAL
+
+
+def test_topk_workspace_and_reports(L):
+    n = ctypes.c_size_t()
+    assert L.sx_logits_topk_workspace_bytes(6, 151936, 40, ctypes.byref(n)) == 0
+    g1 = (151936 + 8191) // 8192
+    assert n.value == 2 * 6 * g1 * 40 * 8 + 6 * g1 * 4
+    e = (ctypes.c_uint32 * 3)(1, 700, 5)
+    assert L.sx_report_expert_error(e, b"layer 3") == sx.SX_EINVAL
+    assert b"expert id 700 at slot 5" in L.sx_last_error()
+    e = (ctypes.c_uint32 * 3)(0, 0, 0)
+    assert L.sx_report_router_error(e, b"x") == sx.SX_OK

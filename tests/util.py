@@ -33,3 +33,53 @@ def max_abs_norm_err(got, ref):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+# ---------------- device helpers (GPU tests) ----------------
+
+def gpu_available():
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+def bf16_dev(bits_u16):
+    """numpy uint16 BF16 bits -> torch.bfloat16 tensor on cuda:0 (the same bits)."""
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits_u16).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def f32_dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def host_bits(t):
+    """A device activation tensor back to numpy: float32, or BF16 bits as uint16."""
+    import torch
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def as_f32(a):
+    return bf16_to_f32(a) if a.dtype == np.uint16 else np.asarray(a, np.float32)
+
+
+def assert_close(got, ref, tol=1e-3, what=""):
+    """The north star's bar: max |got - ref| <= tol * max |ref| (FP32 outputs). BF16 outputs (uint16 bits) may also
+    differ by the one rounding at the store: + 2^-8 |ref| per element."""
+    g = as_f32(got).astype(np.float64)
+    r = as_f32(ref).astype(np.float64)
+    assert g.shape == r.shape, (g.shape, r.shape)
+    assert np.array_equal(np.isnan(g), np.isnan(r)), f"{what}: NaN pattern differs"
+    ok = ~np.isnan(r)
+    if not ok.any():
+        return
+    scale = max(np.max(np.abs(r[ok])), 1e-30)
+    bound = tol * scale + (2.0 ** -8 * np.abs(r[ok]) if got.dtype == np.uint16 else 0.0)
+    err = np.abs(g[ok] - r[ok])
+    worst = float(np.max(err / scale))
+    assert np.all(err <= bound), f"{what}: max-abs-normalised error {worst:.3g} over tolerance {tol}"
