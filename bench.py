@@ -146,7 +146,7 @@ def cpu_baseline(layer, xs, budget_s):
 
     E, k, d, I = layer.E, layer.k, layer.d, layer.I
     Wr = layer.Wr.cpu().numpy()
-    threads = os.cpu_count() or 1
+    threads = min(os.cpu_count() or 1, 16)  # the GPU box's CPU share
     done, t_total = 0, 0.0
     cache = {}
     for r, x in enumerate(xs):
@@ -154,7 +154,7 @@ def cpu_baseline(layer, xs, budget_s):
         # weights the batch touches, copied to the host before the clock starts (they are resident in RAM on a host)
         logits = orc.linear_f32w(xh, Wr)
         ids, coef, _ = orc.moe_router(logits, E, k)
-        touched = np.unique(ids)
+        touched = [int(e) for e in np.unique(ids)]
         for e in touched:
             if e not in cache:
                 cache[e] = (syn.host_rows(layer.gate_up, e * 2 * I, (e + 1) * 2 * I), syn.host_rows(layer.down, e * d, (e + 1) * d))
@@ -232,8 +232,11 @@ def main():
                                   "fp32 router)", "global_batch": 6, "seq_len": 6, "parallelism": "single-gpu"}}
     torch.cuda.synchronize()
     layer, xs, routes = moe_layer_bench(args, out)
+    print(f"moe layer: {out['value']} us/layer, {out['layer_GBps']} GB/s; gate_up kernel "
+          f"{out['roofline']['achieved']} GB/s", file=sys.stderr, flush=True)
     if args.extra:
         extra_configs(out)
+        print(f"configs: {json.dumps(out['configs'])}", file=sys.stderr, flush=True)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(layer, xs, args.cpu_seconds)
     print(json.dumps(out), flush=True)

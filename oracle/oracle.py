@@ -80,6 +80,11 @@ class QWeight:
         self.bits, self.q, self.scale, self.minv = bits, np.ascontiguousarray(q), np.ascontiguousarray(scale), \
             np.ascontiguousarray(minv)
         self.N, self.K, self.G = int(N), int(K), int(G)
+        groups = self.N * (self.K // self.G)
+        need = self.N * self.K // (2 if bits == 4 else 1)
+        if self.q.size != need or self.scale.size != groups or self.minv.size != groups:
+            raise ValueError(f"q{bits} weight [{N}, {K}] G{G}: {self.q.size} code bytes (need {need}), "
+                             f"{self.scale.size}/{self.minv.size} scales/mins (need {groups})")
 
     def args(self):
         return (_ptr(self.q), _ptr(self.scale), _ptr(self.minv))

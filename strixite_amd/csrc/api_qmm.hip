@@ -4,6 +4,8 @@
 #include "common.hpp"
 #include "qmm.hpp"
 
+#include <cstdlib>
+
 namespace sx {
 namespace {
 
@@ -11,9 +13,7 @@ using qmm::Params;
 
 constexpr int64_t kMaxN = 0x7fffffff;
 constexpr int64_t kMaxK = 1 << 24;
-constexpr size_t kLdsBudget = 52 * 1024;  // x staging per block: 3 blocks (12 waves) a CU
-
-int span_codes(int bits) { return bits == 4 ? 128 : 64; }
+constexpr size_t kLdsBudget = 56 * 1024;  // x staging per block: 2 blocks (8 waves) a CU of the 160 KB
 
 // Checks of a weight view shared by every entry point (linear_q4.hip:353-362).
 int check_view(const char *fn, const sx_qview *w, int bits) {
@@ -41,11 +41,6 @@ int check_view(const char *fn, const sx_qview *w, int bits) {
         set_error(cat(fn, ": code array ", (const void *)w->q, " must be 16-byte aligned for vector loads"));
         return SX_EINVAL;
     }
-    if (w->K % span_codes(bits) != 0) {
-        set_error(cat(fn, ": K = ", w->K, " is not a multiple of ", span_codes(bits),
-                      " (the 64-byte row span the gfx950 kernels load)"));
-        return SX_EUNSUPPORTED;
-    }
     return SX_OK;
 }
 
@@ -66,6 +61,7 @@ int tiles_per_chunk(int64_t total_tiles) {
 
 int launch_qmm(const char *fn, int mode, int bits, int act_x, int act_y, Params &p, int64_t units, int64_t rows_out,
                int64_t grid_y, hipStream_t stream) {
+    if (const char *e = getenv("SX_DBG")) p.dbg = atoi(e);
     const int64_t tiles = (rows_out + qmm::kTile - 1) / qmm::kTile;
     p.tiles_per_chunk = tiles_per_chunk(tiles * units);
     p.nchunks = (int)((tiles + p.tiles_per_chunk - 1) / p.tiles_per_chunk);

@@ -53,14 +53,16 @@ struct Params {
     int nchunks;          // row chunks per unit
     int tiles_per_chunk;  // 16-row tiles (SWIGLU: tile pairs) per chunk
     int max_rows;         // LDS rows staged per unit (tokens in a tile; SLOT_COMBINE: A)
+    int dbg;              // TEMP debug flags
 };
 
-// Dynamic LDS bytes for a launch: `rows` staged x rows as nsplit BF16 planes, plus their sums over each run of
-// min(G, span) codes ([blocks][runs][16] FP32; blocks = A for SLOT_COMBINE, else 1).
+// Dynamic LDS bytes for a launch: `rows` staged x rows as nsplit BF16 planes; their sums over each run of min(G, span)
+// codes, padded to whole spans ([blocks][runs][16] FP32; blocks = A for SLOT_COMBINE, else 1); a 2 KB zero block.
 inline size_t lds_bytes(int bits, int nsplit, int64_t K, int64_t G, int rows, int blocks) {
     const int64_t span_codes = bits == 4 ? 128 : 64;
     const int64_t run = G < span_codes ? G : span_codes;
-    return (size_t)nsplit * rows * (K + 8) * 2 + (size_t)blocks * (K / run) * 16 * 4;
+    const int64_t runs = (K + span_codes - 1) / span_codes * (span_codes / run);
+    return (size_t)nsplit * rows * (K + 8) * 2 + (size_t)blocks * runs * 16 * 4 + 2048;
 }
 
 // Launches one mode; bits 4 / 8, act of x and y, nsplit 1 (BF16 x) or 3 (F32 x). grid.x = units * nchunks,

@@ -11,7 +11,8 @@ namespace detail {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPrefetch = 8;  // spans whose loads are in flight per wave
+constexpr int kPrefetch = 8;  // steps (16-byte loads a lane) in flight per wave: one group
+constexpr int kZeroBytes = 2048;  // zero A operand for a group of idle-lane reads (8 q4 spans of BF16)
 
 template <int BITS>
 struct Fmt {
@@ -22,6 +23,14 @@ struct Fmt {
 
 __device__ __forceinline__ uint32_t dword(const uint4 &w, int i) { return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w; }
 
+// (a & mask) | (b & ~mask) in one v_bfi_b32: the code nibbles under the BF16 exponent bits of 128. (gfx9 VOP3
+// takes no literal, so the compiler would otherwise split it into an and and an or.)
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+    return r;
+}
+
 // B operand of MFMA t from a lane's 16 code bytes. q4: dword t's nibbles j = 0..7 (code k0 + j) as BF16 128 + code in
 // element order [0, 4, 1, 5, 2, 6, 3, 7] - one v_and_or (plus a shift) a pair. q8: dwords 2t, 2t+1 in byte order.
 template <int BITS>
@@ -29,10 +38,10 @@ __device__ __forceinline__ bf16x8 codes_b(const uint4 &w, int t) {
     uint4 v;
     if constexpr (BITS == 4) {
         const uint32_t d = dword(w, t);
-        v.x = (d & 0x000F000Fu) | 0x43004300u;
-        v.y = ((d >> 4) & 0x000F000Fu) | 0x43004300u;
-        v.z = ((d >> 8) & 0x000F000Fu) | 0x43004300u;
-        v.w = ((d >> 12) & 0x000F000Fu) | 0x43004300u;
+        v.x = bfi(0x000F000Fu, d, 0x43004300u);
+        v.y = bfi(0x000F000Fu, d >> 4, 0x43004300u);
+        v.z = bfi(0x000F000Fu, d >> 8, 0x43004300u);
+        v.w = bfi(0x000F000Fu, d >> 12, 0x43004300u);
     } else {
         const uint32_t d0 = dword(w, 2 * t), d1 = dword(w, 2 * t + 1);
         auto pair = [](uint32_t d, int b) {  // bytes b, b+1 -> BF16 pair (exact: <= 8 significant bits)
@@ -94,7 +103,8 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
 
     const int64_t K = p.K;
     const int G = p.G;
-    const int nspan = (int)(K / F::kSpanCodes);
+    const int nspan = (int)((K + F::kSpanCodes - 1) / F::kSpanCodes);  // the last span may hold 1-3 quarters
+    const int qlast = (int)(K % F::kSpanCodes) / (F::kSpanCodes / 4);      // its quarters, 0 = all four
     const int run = G < F::kSpanCodes ? G : F::kSpanCodes;     // codes a partial sum covers
     const int nruns = (int)(K / run);
     const int ngs = F::kSpanCodes / run;                         // groups a span
@@ -104,7 +114,8 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
     const int64_t ngroups = K / G;
     const int64_t Nrows = is_swiglu(MODE) ? p.N / 2 : p.N;      // output rows per expert
     const int unit = (int)(blockIdx.x / (unsigned)p.nchunks), chunk = (int)(blockIdx.x % (unsigned)p.nchunks);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps the loop control scalar
 
     // ---- the unit: its activation rows, output rows and expert ----
     if (tid == 0) {
@@ -155,14 +166,14 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
         s_T = T, s_R = R, s_bad = bad;
     }
     __syncthreads();
-    const int T_all = s_T, R = s_R;
+    const int T_all = __builtin_amdgcn_readfirstlane(s_T), R = __builtin_amdgcn_readfirstlane(s_R);
     if (T_all == 0) return;  // an over-provisioned grouped unit: uniform for the block
     const int tiles_total = (int)((Nrows + kTile - 1) / kTile);
     const int tile0 = chunk * p.tiles_per_chunk;
     const int tiles_here = min(p.tiles_per_chunk, tiles_total - tile0);
     if (tiles_here <= 0) return;
 
-    if (s_bad) {  // invalid expert id: NaN outputs, never an out-of-bounds weight read
+    if (__builtin_amdgcn_readfirstlane(s_bad)) {  // invalid expert id: NaN outputs, never an out-of-bounds weight read
         const int64_t rows = (int64_t)tiles_here * kTile;
         for (int64_t i = tid; i < rows * T_all; i += kThreads) {
             const int r = (int)(i / rows);
@@ -176,8 +187,14 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
 
     const int cap = p.max_rows;                               // activation rows staged at once
     const int lds_rows = MODE == SLOT_COMBINE ? R : cap;      // LDS plane height
+    const int nruns_pad = nspan * ngs;                        // run sums padded to whole spans (zeros past K)
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);
     float *xsum = reinterpret_cast<float *>(smem + (size_t)NSPLIT * lds_rows * ldx * 2);
+    uint16_t *zero_block = reinterpret_cast<uint16_t *>(xsum + (size_t)(MODE == SLOT_COMBINE ? R : 1) * nruns_pad * 16);
+    for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<float *>(zero_block)[i] = 0.f;  // A of idle lanes
+    const int pad_entries = (nruns_pad - nruns) * 16;
+    for (int i = tid; i < (MODE == SLOT_COMBINE ? R : 1) * pad_entries; i += kThreads)
+        xsum[(size_t)(i / pad_entries) * nruns_pad * 16 + (size_t)nruns * 16 + i % pad_entries] = 0.f;
     const TX *x = static_cast<const TX *>(p.x);
     const int chunks8 = (int)(K / 8), lanes_per_run = run / 8;
 
@@ -210,13 +227,17 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
         for (int off = 1; off < lanes_per_run; off <<= 1) sum += __shfl_xor(sum, off);
         if (c8 % lanes_per_run == 0) {
             const int rn = c8 / lanes_per_run;
-            if constexpr (MODE == SLOT_COMBINE) xsum[((size_t)r * nruns + rn) * 16] = sum;
+            if constexpr (MODE == SLOT_COMBINE) xsum[((size_t)r * nruns_pad + rn) * 16] = sum;
             else xsum[(size_t)rn * 16 + r] = sum;
         }
     }
     __syncthreads();
 
     // ---- each wave: its tiles of the chunk, every activation pass, all spans (and SLOT_COMBINE's slots) ----
+    // Steps run tile by tile; within a tile pass by pass, segment by segment (SLOT_COMBINE's slots), span by span,
+    // and for SwiGLU gate then up for each span. The loads of step f + kPrefetch are issued when step f is consumed
+    // and nothing reads a loaded value before its step comes up, so the loads stay in flight across spans and tiles.
+    // Loop control is wave-uniform (scalar); row pointers change only at tile / segment boundaries.
     const int n16 = lane & 15, g = lane >> 4;
     const int lg_ngs = ngs == 1 ? 0 : ngs == 2 ? 1 : 2;
     const int gam = (g << lg_ngs) >> 2;             // this lane-quarter's group within a span
@@ -225,53 +246,200 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
     const int npass = (T + TP - 1) / TP;
     const int my_tiles = (tiles_here - wave + kWaves - 1) / kWaves;
     if (my_tiles > 0) {
+    const int per_tile = npass * nseg * nspan * NW;
+    const int total = my_tiles * per_tile;
 
-    // A cursor over the wave's steps (tile i, pass, segment a, span c), span fastest; its row pointers follow it.
-    struct Cursor {
-        int i, pass, a, c;
-        const uint8_t *qrow;
-        const uint16_t *srow, *mrow;
-        int64_t n;
-    };
-    auto place = [&](Cursor &u) {  // row pointers for (i, a)
-        const int64_t tile = tile0 + wave + (int64_t)u.i * kWaves;
-        u.n = tile * kTile + n16;
-        const int64_t nn = u.n < Nrows ? u.n : Nrows - 1;  // partial last tile: a valid row, its result not stored
-        const int64_t row = (MODE == SLOT_COMBINE ? s_wrow[u.a] : s_wrow[0]) + nn;
-        u.qrow = p.q + row * rowbytes + g * 16;
-        u.srow = p.scale + row * ngroups;
-        u.mrow = p.minv + row * ngroups;
-    };
-    auto advance = [&](Cursor &u) {  // wave-uniform branches
-        if (++u.c < nspan) return;
-        u.c = 0;
-        if (++u.a < nseg) return place(u);
-        u.a = 0;
-        if (++u.pass < npass) return place(u);
-        u.pass = 0;
-        ++u.i;
-        place(u);
-    };
-    const int total = my_tiles * npass * nseg * nspan;
-    uint4 wb[kPrefetch][NW];
-    uint32_t sm[kPrefetch][NW];
-    auto issue = [&](const Cursor &u, int slot) {
-        const int gi = ((u.c << lg_ngs) + gam) >> gshift;
+    const uint16_t *xrow0 = xs + (size_t)g * (F::kSpanCodes / 4);
+    const bool a_lane = (n16 / TP) == gam;  // this lane's A row belongs to its quarter's group
+    const int64_t up_q = NW == 2 ? Nrows * rowbytes : 0, up_g = NW == 2 ? Nrows * ngroups : 0;
+    uint4 wb[kPrefetch];
+
+    // ---- fast path: a tile is a whole number of groups (kPrefetch steps), K a whole number of spans, and a span
+    // inside one quantization group. A group never crosses a row, segment or pass, so its kPrefetch steps are
+    // straight-line code with immediate span offsets; the next group's code loads go out as this group's steps are
+    // consumed; and the group's scales and mins arrive as one contiguous window per row (8 or 16 bytes) instead of two
+    // 2-byte loads a step. (q4 K = 4096 / 1024, G = 128 and q8 K = 4096, G = 64 / 128 all qualify.)
+    constexpr int SPG = kPrefetch / NW;                // spans a group
+    const int gpg = SPG >> gshift;                     // quantization groups a group of steps covers (8, 4 or 2)
+    if (per_tile % kPrefetch == 0 && qlast == 0 && ngs == 1 && ngroups % gpg == 0 && nspan % SPG == 0 &&
+        !(p.dbg & 1)) {
+        int ic = 0, ia = 0, ip = 0, ii = 0;  // issue cursor: span, segment, pass, tile
+        const uint8_t *iq;
+        const uint16_t *is_, *im;
+        auto iplace = [&]() {
+            const int64_t n = (int64_t)(tile0 + wave + ii * kWaves) * kTile + n16;
+            const int64_t nn = n < Nrows ? n : Nrows - 1;  // a partial last tile reads a valid row, stores nothing
+            const int64_t row = (MODE == SLOT_COMBINE ? s_wrow[ia] : s_wrow[0]) + nn;
+            iq = p.q + row * rowbytes + g * 16;
+            is_ = p.scale + row * ngroups;
+            im = p.minv + row * ngroups;
+        };
+        iplace();
+        auto issue_slot = [&](int s) {
+            const int span = ic + s / NW, w = s % NW;
+            wb[s] = *reinterpret_cast<const uint4 *>(iq + (w ? up_q : 0) + (int64_t)span * kSpanBytes);
+        };
+        // the scale / min window of the group at the issue cursor: gpg BF16 values from group ic >> gshift
+        uint4 sw_n[NW], mw_n[NW];
+        auto issue_window = [&]() {
+            const int g0 = ic >> gshift;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const int64_t up = w ? Nrows : 0;  // SwiGLU: the up row I rows below the gate row
-            wb[slot][w] = *reinterpret_cast<const uint4 *>(u.qrow + up * rowbytes + (int64_t)u.c * kSpanBytes);
-            sm[slot][w] = (uint32_t)u.srow[up * ngroups + gi] | ((uint32_t)u.mrow[up * ngroups + gi] << 16);
+            for (int w = 0; w < NW; ++w) {
+                const uint16_t *sp_ = is_ + (w ? up_g : 0) + g0, *mp_ = im + (w ? up_g : 0) + g0;
+                if (gpg == 8) {
+                    sw_n[w] = *reinterpret_cast<const uint4 *>(sp_);
+                    mw_n[w] = *reinterpret_cast<const uint4 *>(mp_);
+                } else if (gpg == 4) {
+                    const uint2 a = *reinterpret_cast<const uint2 *>(sp_), b = *reinterpret_cast<const uint2 *>(mp_);
+                    sw_n[w] = uint4{a.x, a.y, 0u, 0u}, mw_n[w] = uint4{b.x, b.y, 0u, 0u};
+                } else {
+                    const uint32_t a = *reinterpret_cast<const uint32_t *>(sp_), b = *reinterpret_cast<const uint32_t *>(mp_);
+                    sw_n[w] = uint4{a, 0u, 0u, 0u}, mw_n[w] = uint4{b, 0u, 0u, 0u};
+                }
+            }
+        };
+        auto advance_issue = [&]() {
+            if (ic + SPG < nspan) {
+                ic += SPG;
+                return;
+            }
+            ic = 0;
+            if (++ia >= nseg) {
+                ia = 0;
+                if (++ip >= npass) ip = 0, ++ii;
+            }
+            iplace();
+        };
+        issue_window();
+#pragma unroll
+        for (int s = 0; s < kPrefetch; ++s) issue_slot(s);
+
+        const int groups = total / kPrefetch;
+        int cc = 0, ca = 0, cp = 0, ci = 0;  // consume cursor
+        f32x4 acc[NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int gr = 0; gr < groups; ++gr) {
+            uint4 sw[NW], mw[NW];
+#pragma unroll
+            for (int w = 0; w < NW; ++w) sw[w] = sw_n[w], mw[w] = mw_n[w];
+            if (gr + 1 < groups) advance_issue();  // the last group re-loads itself (never used)
+            issue_window();
+            const int tok = cp * TP + n16 % TP;
+            const bool a_on = a_lane && tok < T;
+            const int xr = MODE == SLOT_COMBINE ? ca : tok;
+            const uint16_t *xg = xrow0 + (size_t)xr * ldx + (int64_t)cc * F::kSpanCodes;
+            const uint16_t *abase[NSPLIT];
+#pragma unroll
+            for (int sp = 0; sp < NSPLIT; ++sp) abase[sp] = a_on ? xg + (size_t)sp * lds_rows * ldx : zero_block;
+            const float *xsg = MODE == SLOT_COMBINE ? xsum + ((size_t)ca * nruns_pad + cc) * 16
+                                                    : xsum + (size_t)cc * 16 + cp * TP + ((4 * g) & (TP - 1));
+            const float cf = MODE == SLOT_COMBINE ? s_coef[ca] : 1.f;
+#pragma unroll
+            for (int s = 0; s < kPrefetch; ++s) {
+                const int w = s % NW, so = s / NW;  // gate / up; span offset within the group
+                const int gw = so >> gshift;        // its group within the window
+                const uint4 w_cur = wb[s];
+                issue_slot(s);
+                f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < F::kMfmas; ++t) {
+                    const bf16x8 bw = codes_b<BITS>(w_cur, t);
+#pragma unroll
+                    for (int sp = 0; sp < NSPLIT; ++sp) {
+                        const bf16x8 av = *reinterpret_cast<const bf16x8 *>(abase[sp] + so * F::kSpanCodes + t * 8);
+                        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bw, D, 0, 0, 0);
+                    }
+                }
+                const float4 xsv = *reinterpret_cast<const float4 *>(xsg + (size_t)so * 16);
+                const float xv[4] = {xsv.x, xsv.y, xsv.z, xsv.w};
+                const uint32_t swd = dword(sw[w], gw >> 1), mwd = dword(mw[w], gw >> 1);
+                const float s_ = __uint_as_float((gw & 1) ? (swd & 0xFFFF0000u) : (swd << 16));
+                const float m_ = __uint_as_float((gw & 1) ? (mwd & 0xFFFF0000u) : (mwd << 16));
+                const float cm = fmaf(-F::kOff, s_, m_);
+                if constexpr (MODE == SLOT_COMBINE) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[w][v] = fmaf(cf, fmaf(s_, D[v], cm * xv[v]), acc[w][v]);
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[w][v] = fmaf(s_, D[v], fmaf(cm, xv[v], acc[w][v]));
+                }
+            }
+            // consume cursor; at the end of a (tile, pass) the groups' lanes add up and the tile is stored
+            if (cc + SPG < nspan) {
+                cc += SPG;
+                continue;
+            }
+            cc = 0;
+            if (++ca < nseg) continue;
+            ca = 0;
+            const int64_t n = (int64_t)(tile0 + wave + ci * kWaves) * kTile + n16;
+            if (n < Nrows) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int r = cp * TP + 4 * g + v;
+                    if (r >= T) continue;
+                    if constexpr (MODE == COMBINE) {
+                        static_cast<float *>(p.y)[s_out[b0 + r] + n] = acc[0][v];
+                    } else if constexpr (is_swiglu(MODE)) {
+                        TY *h = static_cast<TY *>(p.y);
+                        const float gv = as_stored(acc[0][v], h), uv = as_stored(acc[NW - 1][v], h);
+                        store_act(h, s_out[b0 + r] + n, as_stored(silu(gv), h) * uv);
+                    } else {
+                        store_act(static_cast<TY *>(p.y), s_out[b0 + r] + n, acc[0][v]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) acc[w2] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (++cp >= npass) cp = 0, ++ci;
         }
+    } else {
+    // ---- general path: any K, any tile length; a step at a time ----
+    // Issue cursor: step counters (uniform) and the lane's row pointers (gate row; the up row is Nrows below).
+    int li = 0, lp = 0, la = 0, lc = 0, lw = 0, lf = 0;
+    const uint8_t *lq = nullptr;
+    const uint16_t *ls = nullptr, *lm = nullptr;
+    auto place = [&]() {
+        const int64_t n = (int64_t)(tile0 + wave + li * kWaves) * kTile + n16;
+        const int64_t nn = n < Nrows ? n : Nrows - 1;  // a partial last tile reads a valid row and stores nothing
+        const int64_t row = (MODE == SLOT_COMBINE ? s_wrow[la] : s_wrow[0]) + nn;
+        lq = p.q + row * rowbytes;
+        ls = p.scale + row * ngroups;
+        lm = p.minv + row * ngroups;
     };
-
-    Cursor ld{0, 0, 0, 0, nullptr, nullptr, nullptr, 0}, cu;
-    place(ld);
-    cu = ld;
+    place();
+    auto lnext = [&]() {
+        if (lf + 1 >= total) return;  // past the end: keep re-loading the last step (its data is never used)
+        ++lf;
+        if (NW == 2 && ++lw < 2) return;
+        lw = 0;
+        if (++lc < nspan) return;
+        lc = 0;
+        if (++la >= nseg) {
+            la = 0;
+            if (++lp >= npass) lp = 0, ++li;
+        }
+        place();
+    };
+    const int last_q = (int)rowbytes - 16, last_g = (int)ngroups - 1;
+    uint32_t sb[kPrefetch], mb[kPrefetch];  // raw BF16 scale / min, widened only when consumed
+    // A quarter past K (the last span of a K that is not a whole number of spans) re-reads the row's last 16 bytes
+    // and group: its A operand and run sum are zero, so it adds nothing.
+    auto issue = [&](int slot) {
+        const int qo = min(lc * kSpanBytes + g * 16, last_q);
+        const int gi = min(((lc << lg_ngs) + gam) >> gshift, last_g);
+        const uint8_t *qp = lq + (lw ? up_q : 0);
+        const int64_t go = lw ? up_g : 0;
+        wb[slot] = *reinterpret_cast<const uint4 *>(qp + qo);
+        sb[slot] = ls[go + gi];
+        mb[slot] = lm[go + gi];
+    };
 #pragma unroll
-    for (int s = 0; s < kPrefetch; ++s)
-        if (s < total) issue(ld, s), advance(ld);
+    for (int s = 0; s < kPrefetch; ++s) issue(s), lnext();
 
+    // Consume cursor.
+    int ci = 0, cp = 0, ca = 0, cc = 0;
     f32x4 acc[NW];
 #pragma unroll
     for (int w = 0; w < NW; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -279,84 +447,88 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
     for (int f0 = 0; f0 < total; f0 += kPrefetch) {
 #pragma unroll
         for (int s = 0; s < kPrefetch; ++s) {
-            if (f0 + s >= total) break;
-            uint4 w_cur[NW];
-            uint32_t sm_cur[NW];
-#pragma unroll
-            for (int w = 0; w < NW; ++w) w_cur[w] = wb[s][w], sm_cur[w] = sm[s][w];
-            if (f0 + s + kPrefetch < total) issue(ld, s), advance(ld);
-
+            const int w = NW == 2 ? (s & 1) : 0;  // per_tile and kPrefetch are even with NW = 2: f and s agree
+            const bool live = f0 + s < total;     // wave-uniform; no early exit, so the loop unrolls fully
+            const uint4 w_cur = wb[s];
+            const uint32_t s_cur = sb[s], m_cur = mb[s];
+            issue(s), lnext();
+            if (live) {
             // A operand rows: lane row n16 is token pass*TP + n16 % TP of group n16 / TP; zero unless that group is
-            // this lane-quarter's and the token exists.
-            const int tok = cu.pass * TP + n16 % TP;
-            const bool a_on = (n16 / TP) == gam && tok < T;
-            const int xr = MODE == SLOT_COMBINE ? cu.a : tok;
-            const uint16_t *xa = xs + (size_t)xr * ldx + (int64_t)cu.c * F::kSpanCodes + g * (F::kSpanCodes / 4);
-            f32x4 D[NW];
-#pragma unroll
-            for (int w = 0; w < NW; ++w) D[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+            // this lane-quarter's, the token exists and the quarter lies inside K.
+            const bool q_ok = cc < nspan - 1 || qlast == 0 || g < qlast;
+            const int tok = cp * TP + n16 % TP;
+            const bool a_on = a_lane && tok < T && q_ok;
+            const int xr = MODE == SLOT_COMBINE ? ca : tok;
+            const uint16_t *xa = xrow0 + (size_t)xr * ldx + (int64_t)cc * F::kSpanCodes;
+            f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < F::kMfmas; ++t) {
-                bf16x8 bw[NW];
-#pragma unroll
-                for (int w = 0; w < NW; ++w) bw[w] = codes_b<BITS>(w_cur[w], t);
+                const bf16x8 bw = codes_b<BITS>(w_cur, t);
 #pragma unroll
                 for (int sp = 0; sp < NSPLIT; ++sp) {
-                    bf16x8 av = {};
-                    if (a_on) av = *reinterpret_cast<const bf16x8 *>(xa + (size_t)sp * lds_rows * ldx + t * 8);
-#pragma unroll
-                    for (int w = 0; w < NW; ++w) D[w] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bw[w], D[w], 0, 0, 0);
+                    // lanes with nothing to feed read the zero block (no exec-masked load, no register clearing)
+                    const uint16_t *src = a_on ? xa + (size_t)sp * lds_rows * ldx + t * 8 : zero_block + (t & 1) * 8;
+                    const bf16x8 av = *reinterpret_cast<const bf16x8 *>(src);
+                    D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bw, D, 0, 0, 0);
                 }
             }
-            // Span epilogue: acc += s * D + (min - off * s) * run sum, for this lane's 4 D rows.
-            const int rn = (cu.c << lg_ngs) + gam;
+            // Span epilogue: acc += s * D + (min - off * s) * run sum, for this lane's 4 D rows. The run sums past K
+            // are zero in LDS.
+            const int rn = (cc << lg_ngs) + gam;
             float4 xsv;
-            if constexpr (MODE == SLOT_COMBINE) xsv = *reinterpret_cast<const float4 *>(xsum + ((size_t)cu.a * nruns + rn) * 16);
-            else xsv = *reinterpret_cast<const float4 *>(xsum + (size_t)rn * 16 + cu.pass * TP + ((4 * g) & (TP - 1)));
+            if constexpr (MODE == SLOT_COMBINE) xsv = *reinterpret_cast<const float4 *>(xsum + ((size_t)ca * nruns_pad + rn) * 16);
+            else xsv = *reinterpret_cast<const float4 *>(xsum + (size_t)rn * 16 + cp * TP + ((4 * g) & (TP - 1)));
             const float xv[4] = {xsv.x, xsv.y, xsv.z, xsv.w};
-            const float cf = MODE == SLOT_COMBINE ? s_coef[cu.a] : 1.f;
+            const float s_ = __uint_as_float(s_cur << 16), m_ = __uint_as_float(m_cur << 16);
+            const float cm = fmaf(-F::kOff, s_, m_);
+            if constexpr (MODE == SLOT_COMBINE) {
+                const float cf = s_coef[ca];
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                const float s_ = bf16_to_f32(sm_cur[w] & 0xFFFFu), m_ = bf16_to_f32(sm_cur[w] >> 16);
-                const float cm = m_ - F::kOff * s_;
+                for (int v = 0; v < 4; ++v) acc[w][v] = fmaf(cf, fmaf(s_, D[v], cm * xv[v]), acc[w][v]);
+            } else {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const float part = fmaf(s_, D[w][v], cm * xv[v]);
-                    acc[w][v] = MODE == SLOT_COMBINE ? fmaf(cf, part, acc[w][v]) : acc[w][v] + part;
-                }
+                for (int v = 0; v < 4; ++v) acc[w][v] = fmaf(s_, D[v], fmaf(cm, xv[v], acc[w][v]));
             }
 
-            // End of a (tile, pass): add the groups' lanes, store, reset.
-            if (cu.a == nseg - 1 && cu.c == nspan - 1) {
+            // Advance; at the end of a (tile, pass): add the groups' lanes, store, reset.
+            bool tile_end = false;
+            if (w == NW - 1 && ++cc == nspan) {
+                cc = 0;
+                if (++ca == nseg) ca = 0, tile_end = true;
+            }
+            if (tile_end) {
 #pragma unroll
-                for (int w = 0; w < NW; ++w)
+            for (int w2 = 0; w2 < NW; ++w2)
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        if (ngs >= 4) acc[w][v] += __shfl_xor(acc[w][v], 16);
-                        if (ngs >= 2) acc[w][v] += __shfl_xor(acc[w][v], 32);
-                    }
-                if ((g << lg_ngs) < 4 && cu.n < Nrows) {
+                for (int v = 0; v < 4; ++v) {
+                    if (ngs >= 4) acc[w2][v] += __shfl_xor(acc[w2][v], 16);
+                    if (ngs >= 2) acc[w2][v] += __shfl_xor(acc[w2][v], 32);
+                }
+            const int64_t n = (int64_t)(tile0 + wave + ci * kWaves) * kTile + n16;
+            if ((g << lg_ngs) < 4 && n < Nrows) {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int r = cu.pass * TP + 4 * g + v;
-                        if (r >= T) continue;
-                        if constexpr (MODE == COMBINE) {
-                            static_cast<float *>(p.y)[s_out[b0 + r] + cu.n] = acc[0][v];
-                        } else if constexpr (is_swiglu(MODE)) {
-                            TY *h = static_cast<TY *>(p.y);
-                            const float gv = as_stored(acc[0][v], h), uv = as_stored(acc[1][v], h);
-                            store_act(h, s_out[b0 + r] + cu.n, as_stored(silu(gv), h) * uv);
-                        } else {
-                            store_act(static_cast<TY *>(p.y), s_out[b0 + r] + cu.n, acc[0][v]);
-                        }
+                for (int v = 0; v < 4; ++v) {
+                    const int r = cp * TP + 4 * g + v;
+                    if (r >= T) continue;
+                    if constexpr (MODE == COMBINE) {
+                        static_cast<float *>(p.y)[s_out[b0 + r] + n] = acc[0][v];
+                    } else if constexpr (is_swiglu(MODE)) {
+                        TY *h = static_cast<TY *>(p.y);
+                        const float gv = as_stored(acc[0][v], h), uv = as_stored(acc[NW - 1][v], h);
+                        store_act(h, s_out[b0 + r] + n, as_stored(silu(gv), h) * uv);
+                    } else {
+                        store_act(static_cast<TY *>(p.y), s_out[b0 + r] + n, acc[0][v]);
                     }
                 }
-#pragma unroll
-                for (int w = 0; w < NW; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
-            advance(cu);
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) acc[w2] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (++cp >= npass) cp = 0, ++ci;
+            }  // tile_end
+            }  // live
         }
     }
+    }  // general path
     }  // my_tiles
     }  // token batches
 }

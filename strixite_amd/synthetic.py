@@ -34,6 +34,7 @@ def router_weight(E, K, seed, device="cuda"):
 
 def host_rows(w, r0, r1):
     """Host numpy copy (q, scale, minv) of weight rows [r0, r1): for the oracle on the rows a test touches."""
+    r0, r1 = int(r0), int(r1)  # numpy integers would overflow int32 on the byte offsets of large weights
     per = w.K // (2 if w.bits == 4 else 1)
     groups = w.K // w.G
     q = w.q[r0 * per:r1 * per].cpu().numpy()

@@ -59,3 +59,10 @@ def test_linear_rejects_misaligned_x():
     x = torch.zeros(2 * 128 + 1, dtype=torch.bfloat16, device="cuda")[1:].view(2, 128)
     with pytest.raises(SxError, match="16-byte aligned"):
         kx.linear(x, w)
+
+
+@pytest.mark.parametrize("bits,K,G", [(4, 96, 32), (4, 64, 64), (4, 320, 64), (8, 96, 32), (8, 32, 32)])
+def test_linear_k_not_a_whole_span(bits, K, G):
+    """K that ends inside the kernels' 64-byte row span (the reference allows any K % G == 0)."""
+    got, ref = run(bits, 24, K, G, 3, BF16, F32, seed=K)
+    util.assert_close(got, ref, what=f"q{bits} K{K} G{G}")

@@ -97,7 +97,7 @@ def test_group_routes_invariants():
 
 def make_experts(seed, E, I, d, G=128):
     rng = np.random.default_rng(seed)
-    return util.rand_qweight(rng, 4, E * 2 * I, d, G), util.rand_qweight(rng, 4, E * d, I, G), rng
+    return util.rand_qweight(rng, 4, E * 2 * I, d, G), util.rand_qweight(rng, 4, E * d, I, min(G, I)), rng
 
 
 @pytest.mark.parametrize("act", [orc.BF16, orc.F32])

@@ -74,7 +74,10 @@ def assert_close(got, ref, tol=1e-3, what=""):
     g = as_f32(got).astype(np.float64)
     r = as_f32(ref).astype(np.float64)
     assert g.shape == r.shape, (g.shape, r.shape)
-    assert np.array_equal(np.isnan(g), np.isnan(r)), f"{what}: NaN pattern differs"
+    if not np.array_equal(np.isnan(g), np.isnan(r)):
+        bad = np.argwhere(np.isnan(g) != np.isnan(r))
+        raise AssertionError(f"{what}: NaN pattern differs: {int(np.isnan(g).sum())} NaN on the GPU, "
+                             f"{int(np.isnan(r).sum())} in the oracle, first at {bad[:4].tolist()}")
     ok = ~np.isnan(r)
     if not ok.any():
         return
