@@ -7,10 +7,12 @@ namespace sx {
 namespace {
 
 // ---------------- router projection: y[M, N] = x[M, K] . W[N, K]^T, FP32 weights ----------------
-// A wave per output row n, 4 rows a block; the block's x rows (8 BF16 or 4 FP32 tokens) are staged in LDS. Each lane
-// walks the row in float4 steps (coalesced 1 KB per wave step) and keeps one FP32 accumulator per token; the wave
-// reduction at the end is a butterfly. Further tokens run in further grid rows.
-constexpr int kF32wTokens = 8;
+// The router weight (E x d FP32, 8 MB at E = 512, d = 4096) is read once; it is the whole cost. A block takes kF32wRows
+// weight rows and NT tokens; each thread owns every 256th float4 column of those rows, issues all of its weight loads
+// before it uses any (K = 4096: 4 float4 a row in flight a thread), and reads the tokens' x values straight from
+// L2 (x is a few KB a token). Per (row, token) the thread's partial sum goes through a wave butterfly and the four
+// waves' sums through LDS. Further tokens run in further grid rows.
+constexpr int kF32wTokens = 8, kF32wRows = 2, kF32wUnroll = 4;
 
 template <typename TX>
 __device__ __forceinline__ float4 load4(const TX *p) {
@@ -23,38 +25,63 @@ __device__ __forceinline__ float4 load4(const TX *p) {
     }
 }
 
-// x rows are staged in LDS in their own dtype (BF16: 8 tokens x K = 4096 in 64 KB).
 template <typename TX, int NT>
 __global__ void __launch_bounds__(256) linear_f32w_kernel(const TX *x, const float *W, float *y, int64_t M, int64_t N,
                                                           int64_t K) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-    TX *xs = reinterpret_cast<TX *>(smem_raw);  // [tokens][K]
-    const int64_t m0 = (int64_t)blockIdx.y * NT;
+    __shared__ float part[4][kF32wRows * NT];
+    const int64_t m0 = (int64_t)blockIdx.y * NT, n0 = (int64_t)blockIdx.x * kF32wRows;
     const int T = (int)min((int64_t)NT, M - m0);
-    for (int64_t i = threadIdx.x; i < (int64_t)T * K; i += blockDim.x) xs[i] = x[m0 * K + i];
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t n = (int64_t)blockIdx.x * 4 + wave;
-    if (n >= N) return;  // after the only barrier
-    float acc[NT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t K4 = K / 4;
+    const float4 *wr[kF32wRows];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.f;
-    const float4 *wr = reinterpret_cast<const float4 *>(W + n * K);
-    for (int64_t k4 = lane; k4 < K / 4; k4 += 64) {
-        const float4 w = wr[k4];
+    for (int r = 0; r < kF32wRows; ++r) wr[r] = reinterpret_cast<const float4 *>(W + min(n0 + r, N - 1) * K);
+    float acc[kF32wRows][NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t < T) {
-                const float4 xv = load4(xs + (int64_t)t * K + 4 * k4);
-                acc[t] = fmaf(w.x, xv.x, fmaf(w.y, xv.y, fmaf(w.z, xv.z, fmaf(w.w, xv.w, acc[t]))));
+    for (int r = 0; r < kF32wRows; ++r)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[r][t] = 0.f;
+    // Every load is unconditional (clamped column and token, the weight zeroed past K) so that none waits for another.
+    const TX *xt[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) xt[t] = x + (m0 + min(t, T - 1)) * K;
+    for (int64_t base = 0; base < K4; base += 256 * kF32wUnroll) {
+        float4 w[kF32wUnroll][kF32wRows], xv[kF32wUnroll][NT];
+#pragma unroll
+        for (int u = 0; u < kF32wUnroll; ++u) {
+            const int64_t k4 = min(base + u * 256 + tid, K4 - 1);
+#pragma unroll
+            for (int r = 0; r < kF32wRows; ++r) w[u][r] = wr[r][k4];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) xv[u][t] = load4(xt[t] + 4 * k4);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first use
+#pragma unroll
+        for (int u = 0; u < kF32wUnroll; ++u) {
+            const float on = base + u * 256 + tid < K4 ? 1.f : 0.f;
+#pragma unroll
+            for (int r = 0; r < kF32wRows; ++r) {
+                const float4 wv = float4{w[u][r].x * on, w[u][r].y * on, w[u][r].z * on, w[u][r].w * on};
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    acc[r][t] = fmaf(wv.x, xv[u][t].x, fmaf(wv.y, xv[u][t].y,
+                                     fmaf(wv.z, xv[u][t].z, fmaf(wv.w, xv[u][t].w, acc[r][t]))));
             }
         }
     }
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-        for (int off = 32; off > 0; off >>= 1) acc[t] += __shfl_xor(acc[t], off);
-    if (lane == 0)
-        for (int t = 0; t < T; ++t) y[(m0 + t) * N + n] = acc[t];
+    for (int r = 0; r < kF32wRows; ++r)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float v = acc[r][t];
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0) part[wave][r * NT + t] = v;
+        }
+    __syncthreads();
+    if (tid < kF32wRows * NT) {
+        const int r = tid / NT, t = tid % NT;
+        if (t < T && n0 + r < N) y[(m0 + t) * N + n0 + r] = part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
+    }
 }
 
 // ---------------- top-k router ----------------
@@ -68,9 +95,30 @@ __device__ __forceinline__ uint64_t route_key(float v, int idx) {
     return ((uint64_t)hi << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
+// The logit a key was made from (a -0 logit comes back as +0, which no later use tells apart).
+__device__ __forceinline__ float key_value(uint64_t key) {
+    const uint32_t hi = (uint32_t)(key >> 32);
+    return __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
+}
+
+// Wave-wide maximum of 64-bit keys. Within a row of 16 lanes the partners come through DPP (quad [1,0,3,2],
+// quad [2,3,0,1], half-row mirror, row mirror: after each step every lane holds the maximum over 2, 4, 8, 16 lanes,
+// since max needs no particular pairing); across the four rows two LDS-routed shuffles.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_max(uint64_t k) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, 0xF, 0xF, false);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    return o > k ? o : k;
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+    k = dpp_max<0xB1>(k);   // quad_perm [1,0,3,2]
+    k = dpp_max<0x4E>(k);   // quad_perm [2,3,0,1]
+    k = dpp_max<0x141>(k);  // row_half_mirror
+    k = dpp_max<0x140>(k);  // row_mirror
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
+    for (int off = 16; off <= 32; off <<= 1) {
         const uint32_t lo = __shfl_xor((uint32_t)k, off), hi = __shfl_xor((uint32_t)(k >> 32), off);
         const uint64_t o = ((uint64_t)hi << 32) | lo;
         k = o > k ? o : k;
@@ -124,7 +172,7 @@ __global__ void __launch_bounds__(64) moe_router_kernel(const T *logits, int64_t
     for (int r = 0; r < k; ++r) {
         const uint64_t best = wave_max_u64(mine);
         const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
-        const float bv = load_act(row, bi);
+        const float bv = key_value(best);
         if (r == 0) top = bv;
         if (lane == r) my_v = bv, my_i = bi;
         if ((bi & 63) == lane) {  // the picked expert is this lane's
@@ -162,17 +210,15 @@ int sx_linear_f32w(const void *x, const float *W, int64_t N, int64_t K, float *y
     SX_CHECK(N >= 1 && K >= 4 && K % 4 == 0 && M >= 1, "N = ", N, ", K = ", K, " (a positive multiple of 4), M = ", M);
     SX_CHECK(aligned(W, 16) && aligned(x, 8), "W must be 16-byte and x 8-byte aligned");
     SX_CHECK(act == SX_ACT_F32 || act == SX_ACT_BF16, "unsupported activation dtype ", act);
-    const int nt = act == SX_ACT_F32 ? kF32wTokens / 2 : kF32wTokens;
-    const size_t lds = (size_t)nt * K * act_bytes(act);
-    SX_CHECK(lds <= 64 * 1024, "K = ", K, " too long for the LDS-staged projection");
-    SX_CHECK((M + nt - 1) / nt <= 65535, "M = ", M, " too large");
+    SX_CHECK((M + kF32wTokens - 1) / kF32wTokens <= 65535, "M = ", M, " too large");
+    SX_CHECK((N + kF32wRows - 1) / kF32wRows <= 0x7fffffff, "N = ", N, " too large");
     SX_CHECK(apart(y, M * N * 4, x, M * K * act_bytes(act)) && apart(y, M * N * 4, W, N * K * 4), "y overlaps inputs");
-    const dim3 grid((unsigned)((N + 3) / 4), (unsigned)((M + nt - 1) / nt));
+    const dim3 grid((unsigned)((N + kF32wRows - 1) / kF32wRows), (unsigned)((M + kF32wTokens - 1) / kF32wTokens));
     if (act == SX_ACT_F32)
-        linear_f32w_kernel<float, kF32wTokens / 2><<<grid, 256, lds, stream_of(stream)>>>(static_cast<const float *>(x), W,
-                                                                                          y, M, N, K);
+        linear_f32w_kernel<float, kF32wTokens><<<grid, 256, 0, stream_of(stream)>>>(static_cast<const float *>(x), W, y,
+                                                                                   M, N, K);
     else
-        linear_f32w_kernel<uint16_t, kF32wTokens><<<grid, 256, lds, stream_of(stream)>>>(
+        linear_f32w_kernel<uint16_t, kF32wTokens><<<grid, 256, 0, stream_of(stream)>>>(
             static_cast<const uint16_t *>(x), W, y, M, N, K);
     SX_LAUNCHED("linear_f32w M=", M, " N=", N, " K=", K);
     return SX_OK;
