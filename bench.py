@@ -20,6 +20,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "µs/layer for q4 MoE verify at M=6 + achieved HBM GB/s; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_JSON = os.path.join("profiles", "hbm_traffic_cfg3.json")
+COPY_PROBE_BYTES = 256 << 20  # FP32 elements read and written once by the calibration kernel
 
 
 def parse():
@@ -30,6 +32,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--extra", action="store_true", help="also time configs 1, 2 and 5")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--probe", action="store_true",
+                    help="for rocprofv3 --pmc: a plain copy kernel of known size (the counters' calibration), then the "
+                         "config-3 gate_up and down kernels alone, and exit")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two --probe counter runs (FETCH_SIZE, WRITE_SIZE) into " + TRAFFIC_JSON)
     return ap.parse_args()
 
 
@@ -115,8 +122,13 @@ def moe_layer_bench(args, out):
     ms = time_launches(gate_up, n)
     gu_bytes = sum(Us[i % R] * gu_per_expert + M * d * 2 + M * k * I * 2 for i in range(n)) / n
     achieved = gu_bytes / (ms * 1e-3) / 1e9
+    traffic = None
+    tj = os.path.join(ROOT, TRAFFIC_JSON)
+    if os.path.exists(tj):  # HBM bytes a launch, measured by rocprofv3 counters (see --probe / --pmc-summary)
+        with open(tj) as f:
+            traffic = json.load(f).get("gate_up", {}).get("hbm_bytes_per_launch")
     out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                        "kernel": "qmm_kernel SWIGLU (grouped gate_up + SwiGLU)", "avg_launch_us": round(ms * 1e3, 3),
                        "algorithmic_bytes_per_launch": int(gu_bytes)}
 
@@ -214,8 +226,89 @@ def extra_configs(out):
     out["configs"] = res
 
 
+def probe():
+    """A plain copy kernel of known size (read COPY_PROBE_BYTES, write COPY_PROBE_BYTES), then the config-3 gate_up
+    and down kernels alone over the rotating routes. Run under rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE)."""
+    import torch
+
+    from strixite_amd import kernels as kx
+    from strixite_amd import synthetic as syn
+    from strixite_amd.verify import MoeVerifyLayer
+
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads src, writes dst
+    torch.cuda.synchronize()
+    del src, dst
+    E, d, I, k, M, R = 512, 4096, 1024, 10, 6, 16
+    Wr = syn.router_weight(E, d, seed=11)
+    gu = syn.qweight(4, E * 2 * I, d, 128, seed=12)
+    dn = syn.qweight(4, E * d, I, 128, seed=13)
+    xs = [syn.activations(M, d, seed=100 + r) for r in range(R)]
+    layer = MoeVerifyLayer(Wr, gu, dn, E, k, M)
+    routes, Us = [], []
+    for r in range(R):
+        layer.forward(xs[r])
+        ids = layer.ids.clone()
+        routes.append((ids, layer.coef.clone(), kx.group_routes(ids, E)[0]))
+        Us.append(int(torch.unique(ids).numel()))
+    h = torch.empty((M, k, I), dtype=torch.bfloat16, device="cuda")
+    yb = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
+    part = torch.empty((M * k, d), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(R):
+        kx.gather_grouped(xs[i], gu, E, routes[i][2], M, k, swiglu=True, y=h)
+    for i in range(R):
+        kx.combine_grouped(h, dn, E, routes[i][0], routes[i][1], routes[i][2], partial=part, y=yb)
+    torch.cuda.synchronize()
+    alg = {"gate_up": sum(U * (gu.nbytes() // E) + M * d * 2 + M * k * I * 2 for U in Us) / R,
+           "down": sum(U * (dn.nbytes() // E) + M * k * I * 2 + M * k * d * 4 for U in Us) / R}
+    print(json.dumps({"probe": "done", "algorithmic_bytes_per_launch": alg, "distinct_experts": Us}))
+
+
+def pmc_summary(fetch_dir, write_dir):
+    """Per-launch HBM traffic of the probe's kernels from two rocprofv3 counter runs, each scaled by what the same
+    counter reads for the copy kernel (COPY_PROBE_BYTES read and written)."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        rows, copies = {}, []
+        for fn in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(fn)):
+                if r["Counter_Name"] != counter:
+                    continue
+                name, v = r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0  # KiB -> bytes
+                if "MulFunctor" in name:
+                    copies.append((int(r["Grid_Size"]), v))
+                key = "gate_up" if "qmm_kernel<4, 1, 2," in name else "down" if "qmm_kernel<4, 1, 3," in name else None
+                if key:
+                    rows.setdefault(key, []).append(v)
+        big = max(g for g, _ in copies)  # the copy probe: the largest multiply launched
+        rows["copy"] = [v for g, v in copies if g == big]
+        return {k: sum(v) / len(v) for k, v in rows.items()}
+
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    f_scale, w_scale = COPY_PROBE_BYTES / fetch["copy"], COPY_PROBE_BYTES / write["copy"]
+    out = {"copy_probe_bytes": COPY_PROBE_BYTES, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+           "note": "FETCH_SIZE / WRITE_SIZE (KiB a dispatch) times the factor that makes the copy kernel read and "
+                   "write exactly copy_probe_bytes"}
+    for k in ("gate_up", "down"):
+        fb, wb = fetch[k] * f_scale, write[k] * w_scale
+        out[k] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "hbm_bytes_per_launch": int(fb + wb),
+                  "raw_fetch_kib": round(fetch[k] / 1024, 1), "raw_write_kib": round(write[k] / 1024, 1)}
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    with open(os.path.join(ROOT, TRAFFIC_JSON), "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported (multi-GPU is a "
                                    "design note only)", "n_gpus": args.gpus}))
@@ -224,6 +317,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     import strixite_amd
     strixite_amd.lib()  # fails loudly without the built library
+    if args.probe:
+        probe()
+        return
 
     out = {"metric": METRIC, "value": None, "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": False, "scaling": "weak",

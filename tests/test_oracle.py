@@ -82,6 +82,42 @@ def test_linear_bf16_to_f32_rowsums():
     np.testing.assert_allclose(y, np.tile(orc.dequant(w).astype(np.float64).sum(1), (2, 1)), rtol=1e-6)
 
 
+def test_linear_f32w_basis_vectors_and_brute_force():
+    """The FP32-weight router projection: x = e_k returns column k of W exactly, and random x agrees with a float64
+    matrix product (a transposed operand or a dropped row fails both)."""
+    rng = np.random.default_rng(9)
+    W = (rng.standard_normal((24, 96)) * 0.02).astype(np.float32)
+    for k in (0, 5, 95):
+        x = np.zeros((1, 96), np.float32)
+        x[0, k] = 1.0
+        assert np.array_equal(orc.linear_f32w(x, W)[0], W[:, k])
+        assert np.array_equal(orc.linear_f32w(util.f32_to_bf16(x), W)[0], W[:, k])  # 1.0 is exact in BF16
+    x = rng.standard_normal((5, 96)).astype(np.float32)
+    np.testing.assert_allclose(orc.linear_f32w(x, W), x.astype(np.float64) @ W.astype(np.float64).T, rtol=1e-6,
+                               atol=1e-7)
+
+
+def test_swiglu_limits_and_bf16_rounding_points():
+    """silu(v) = v / (1 + e^-v): 0 at 0, v for large v, -0 side for very negative v, silu(1) = 1/(1 + 1/e); a swapped
+    gate / up or a missing sigmoid fails. BF16 rounds twice: bf16(bf16(silu(g)) * u) (kernels/swiglu.hip:31-36)."""
+    g = np.array([[0.0, 30.0, -30.0, 1.0]], np.float32)
+    u = np.array([[5.0, 2.0, 3.0, 1.0]], np.float32)
+    h = orc.swiglu(np.concatenate([g, u], axis=1))[0]
+    assert h[0] == 0.0 and h[1] == np.float32(60.0) and abs(h[2]) < 1e-11
+    assert h[3] == np.float32(1.0 / (1.0 + np.exp(-1.0)))
+    rng = np.random.default_rng(10)
+    gb = util.f32_to_bf16(rng.standard_normal((3, 64)).astype(np.float32))
+    ub = util.f32_to_bf16(rng.standard_normal((3, 64)).astype(np.float32))
+    hb = orc.swiglu(np.concatenate([gb, ub], axis=1))
+    gf, uf = util.bf16_to_f32(gb).astype(np.float64), util.bf16_to_f32(ub).astype(np.float64)
+    silu = util.f32_to_bf16((gf / (1.0 + np.exp(-gf))).astype(np.float32))
+    want = util.f32_to_bf16((util.bf16_to_f32(silu).astype(np.float64) * uf).astype(np.float32))
+    # float64 silu rounded to f32 can differ from the f32 expf path by one f32 ulp, which may move a BF16 rounding
+    # tie; allow one BF16 ulp on at most a few elements, exact elsewhere
+    diff = np.abs(hb.astype(np.int32) - want.astype(np.int32))
+    assert diff.max() <= 1 and (diff > 0).sum() <= 3
+
+
 # ---------------- router (a5) ----------------
 
 def _router_by_lexsort(logits, k):
