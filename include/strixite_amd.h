@@ -86,6 +86,12 @@ int sx_moe_shared_add_inject(void *y, const void *s, const float *gate_logit, in
 int sx_moe_route_workspace_bytes(int64_t M, int64_t A, int64_t E, size_t *bytes);
 int sx_moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void *ws, size_t ws_bytes, uint32_t *err,
                         sx_stream stream);
+/* moe_router (no shared slot) then moe_group_routes in one launch, for M*k <= 2048: the same ids, coef, error words
+ * and workspace as those two calls (kernels/moe_router.hpp:38-40 + kernels/moe_grouped.hpp:47-49, the sequence
+ * runtime/qwen4exp.cpp:1139-1147 runs at verify width). No reference counterpart as one call. */
+int sx_moe_router_group(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int act, int32_t *ids,
+                        float *coef, uint32_t *router_err, void *ws, size_t ws_bytes, uint32_t *expert_err,
+                        sx_stream stream);
 /* y [M, A, N] (linear_q4_experts_gather_grouped, moe_grouped.hpp:53-55). */
 int sx_linear_q4_experts_gather_grouped(const void *x, const sx_qview *w, int64_t E, const void *ws, size_t ws_bytes,
                                         int64_t M, int64_t A, void *y, int act, int math, sx_stream stream);

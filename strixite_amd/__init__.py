@@ -65,6 +65,7 @@ SIGNATURES = {
     "sx_linear_q4_experts_gather_swiglu_grouped": [_P, _QV, _I64, _P, ctypes.c_size_t, _I64, _I64, _P, _INT, _P],
     "sx_swiglu": [_P, _P, _I64, _I64, _INT, _P],
     "sx_linear_f32w": [_P, _P, _I64, _I64, _P, _I64, _INT, _P],
+    "sx_moe_router_group": [_P, _I64, _I64, _I64, _I64, _INT, _P, _P, _P, _P, ctypes.c_size_t, _P, _P],
     "sx_logits_topk_workspace_bytes": [_I64, _I64, _I64, _SZP],
     "sx_logits_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_size_t, _P, _I64, _P],
     "sx_mtp_pick": [_P, _I64, _P, _P, _P, _P, _P, _P],

@@ -123,6 +123,19 @@ int launch_qmm(const char *fn, int mode, int bits, int act_x, int act_y, Params 
                 const int c = per_cu[(h[b * 16 + 9] << 32) | ((h[b * 16 + 8] >> 8) & 0xFF)];
                 by[c].first += (h[b * 16 + 4] - t0) * 0.01, by[c].second++;
             }
+            std::map<int, std::pair<double, int>> byx, byse;
+            for (size_t b = 0; b < nw; b += 4) {
+                if (!h[b * 16 + 4]) continue;
+                const int xcc = (int)(h[b * 16 + 9] & 0xF), se = (int)((h[b * 16 + 8] >> 13) & 0x7);
+                const double e = (h[b * 16 + 4] - t0) * 0.01;
+                byx[xcc].first += e, byx[xcc].second++;
+                byse[xcc * 8 + se].first += e, byse[xcc * 8 + se].second++;
+            }
+            fprintf(stderr, "  by XCC:");
+            for (auto &kv : byx) fprintf(stderr, " x%d %d blk %.1f;", kv.first, kv.second.second, kv.second.first / kv.second.second);
+            fprintf(stderr, "\n  by XCC.SE:");
+            for (auto &kv : byse) fprintf(stderr, " %d.%d:%d/%.1f", kv.first / 8, kv.first % 8, kv.second.second, kv.second.first / kv.second.second);
+            fprintf(stderr, "\n");
             fprintf(stderr, "  CUs used %zu;", per_cu.size());
             for (auto &kv : by) fprintf(stderr, " %d blocks/CU: %d blocks, mean end %.2f us;", kv.first, kv.second.second, kv.second.first / kv.second.second);
             fprintf(stderr, "\n");

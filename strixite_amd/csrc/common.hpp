@@ -104,6 +104,13 @@ inline int act_bytes(int act) { return act == SX_ACT_F32 ? 4 : 2; }
 // Number of compute units of the current device (cached per device).
 int device_cus();
 
+// The route workspace (kernels/moe_grouped.hip:63-81) for S = M * A slots over E experts, in int32 words.
+struct Layout {
+    int64_t S, E, Tmax, WTmax;
+    int64_t ints() const { return 4 + (E + 2) + S + 2 * Tmax + 2 * WTmax; }
+};
+Layout layout_of(int64_t M, int64_t A, int64_t E);
+
 // y[m, n] = sum_a coef[m, a] * partial[m * A + a, n], a in order, rounded once; NaN rows for tokens with a bad id
 // (the grouped combine's second step, route.hip).
 int combine_reduce(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,

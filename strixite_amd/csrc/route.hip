@@ -1,6 +1,7 @@
 // Route grouping (moe_group_routes), the grouped combine's reduction, SwiGLU, the shared-expert add, and the C-ABI's
 // error channel.
 #include "common.hpp"
+#include "route_impl.hpp"
 
 #include <climits>
 #include <mutex>
@@ -39,97 +40,14 @@ namespace {
 // tile_bucket [Tmax], tile_start [Tmax] (16-slot tiles), wtile_bucket [WTmax], wtile_start [WTmax] (64-slot tiles);
 // Tmax = S / 16 + E + 2, WTmax = S / 64 + E + 2 (a bucket of c slots has ceil(c / R) <= c / R + 1 tiles).
 constexpr int kRouteThreads = 1024;  // one bucket a thread: E <= 1023 experts + the invalid-id bucket
-constexpr int kR = 16, kRW = 64;
-
-struct Layout {
-    int64_t S, E, Tmax, WTmax;
-    int64_t ints() const { return 4 + (E + 2) + S + 2 * Tmax + 2 * WTmax; }
-};
-Layout layout_of(int64_t M, int64_t A, int64_t E) {
-    const int64_t S = M * A;
-    return {S, E, S / kR + E + 2, S / kRW + E + 2};
-}
-
-// Exclusive prefix sums of three per-thread counts over the 1024-thread block: wave64 inclusive scans by shuffles,
-// then the 16 wave totals scanned by one wave.
-__device__ void block_scan3(int (&v)[3], int (&excl)[3], int (&total)[3], int (*wtot)[3]) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int inc[3] = {v[0], v[1], v[2]};
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int o = __shfl_up(inc[j], off);
-            if (lane >= off) inc[j] += o;
-        }
-    if (lane == 63)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) wtot[wave][j] = inc[j];
-    __syncthreads();
-    if (wave == 0) {
-        int w[3];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) w[j] = lane < kRouteThreads / 64 ? wtot[lane][j] : 0;
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1)
-#pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const int o = __shfl_up(w[j], off);
-                if (lane >= off) w[j] += o;
-            }
-        if (lane < kRouteThreads / 64)
-#pragma unroll
-            for (int j = 0; j < 3; ++j) wtot[lane][j] = w[j];  // inclusive wave prefix
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int before = wave ? wtot[wave - 1][j] : 0;
-        excl[j] = before + inc[j] - v[j];
-        total[j] = wtot[kRouteThreads / 64 - 1][j];
-    }
-}
 
 __global__ void __launch_bounds__(kRouteThreads)
     route_kernel(const int32_t *ids, int S, int E, int Tmax, int WTmax, int32_t *ws, uint32_t *err) {
     __shared__ int cnt[kRouteThreads], cursor[kRouteThreads];
     __shared__ int wtot[kRouteThreads / 64][3];
     __shared__ int first_bad;
-    const int t = threadIdx.x;
-    cnt[t] = 0;
-    if (t == 0) first_bad = INT_MAX;
-    __syncthreads();
-    for (int s = t; s < S; s += kRouteThreads) {
-        const int32_t id = ids[s];
-        const bool bad = id < 0 || id >= E;
-        atomicAdd(&cnt[bad ? E : id], 1);
-        if (bad) atomicMin(&first_bad, s);
-    }
-    __syncthreads();
-    // The first invalid slot in slot order (an atomic minimum, so independent of scheduling) is what err reports.
-    if (t == 0 && first_bad != INT_MAX) flag_error(err, (uint32_t)ids[first_bad], (uint32_t)first_bad);
-    const int count = t <= E ? cnt[t] : 0;
-    int v[3] = {count, (count + kR - 1) / kR, (count + kRW - 1) / kRW}, ex[3], tot[3];
-    block_scan3(v, ex, tot, wtot);
-    int32_t *offsets = ws + 4, *slots = offsets + E + 2, *tile_bucket = slots + S, *tile_start = tile_bucket + Tmax;
-    int32_t *wtile_bucket = tile_start + Tmax, *wtile_start = wtile_bucket + WTmax;
-    if (t <= E) {
-        offsets[t] = ex[0];
-        cursor[t] = ex[0];
-        for (int i = 0; i < v[1]; ++i) tile_bucket[ex[1] + i] = t, tile_start[ex[1] + i] = ex[0] + i * kR;
-        for (int i = 0; i < v[2]; ++i) wtile_bucket[ex[2] + i] = t, wtile_start[ex[2] + i] = ex[0] + i * kRW;
-    }
-    if (t == 0) {
-        ws[0] = tot[1], ws[1] = S, ws[2] = E, ws[3] = tot[2];
-        offsets[E + 1] = tot[0];
-    }
-    __syncthreads();
-    // Placement through per-bucket cursors: the order within a bucket follows the atomics; no output depends on it
-    // (every grouped output row is computed from its own slot's input row).
-    for (int s = t; s < S; s += kRouteThreads) {
-        const int32_t id = ids[s];
-        slots[atomicAdd(&cursor[(id < 0 || id >= E) ? E : id], 1)] = s;
-    }
+    routing::group_in_block<kRouteThreads>([&](int s) { return ids[s]; }, S, E, Tmax, WTmax, ws, err, cnt, cursor,
+                                           wtot, &first_bad);
 }
 
 // ---------------- combine reduce ----------------
@@ -194,6 +112,11 @@ int grid_for(int64_t n, int64_t cap = 65535ll * 16) {
 }
 
 }  // namespace
+
+Layout layout_of(int64_t M, int64_t A, int64_t E) {
+    const int64_t S = M * A;
+    return {S, E, S / routing::kR + E + 2, S / routing::kRW + E + 2};
+}
 
 int combine_reduce(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                    int64_t N, void *y, int act, hipStream_t stream) {

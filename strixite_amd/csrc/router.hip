@@ -1,5 +1,6 @@
 // MoE routing on gfx950: the router projection (FP32 weights) and the top-k router (kernels/moe_router.hpp:11-40).
 #include "common.hpp"
+#include "route_impl.hpp"
 
 #include <climits>
 
@@ -26,9 +27,8 @@ __device__ __forceinline__ float4 load4(const TX *p) {
 }
 
 template <typename TX, int NT>
-__global__ void __launch_bounds__(256) linear_f32w_kernel(const TX *x, const float *W, float *y, int64_t M, int64_t N,
-                                                          int64_t K) {
-    __shared__ float part[4][kF32wRows * NT];
+__device__ __forceinline__ void project_rows(const TX *x, const float *W, float *y, int64_t M, int64_t N, int64_t K,
+                                             float (*part)[kF32wRows * NT]) {
     const int64_t m0 = (int64_t)blockIdx.y * NT, n0 = (int64_t)blockIdx.x * kF32wRows;
     const int T = (int)min((int64_t)NT, M - m0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -69,14 +69,28 @@ __global__ void __launch_bounds__(256) linear_f32w_kernel(const TX *x, const flo
             }
         }
     }
+    // Wave reduction of the kF32wRows * NT (= 16) sums: halve the vector at each of the xor-32, 16, 8, 4 steps (a
+    // lane keeps the half its lane bit selects and adds its partner's copy of it), then xor 2 and 1 on the last
+    // value: 17 shuffles instead of 6 a sum. Lane bits 5..2 then name the sum a lane holds.
+    static_assert(kF32wRows * NT == 16, "the reduction halves 16 sums");
+    float v16[16];
 #pragma unroll
     for (int r = 0; r < kF32wRows; ++r)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float v = acc[r][t];
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-            if (lane == 0) part[wave][r * NT + t] = v;
+        for (int t = 0; t < NT; ++t) v16[r * NT + t] = acc[r][t];
+#pragma unroll
+    for (int n = 8, bit = 32; n >= 1; n >>= 1, bit >>= 1) {
+        const bool upper = (lane & bit) != 0;
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+            const float keep = upper ? v16[n + i] : v16[i], give = upper ? v16[i] : v16[n + i];
+            v16[i] = keep + __shfl_xor(give, bit);
         }
+    }
+    float tot = v16[0];
+    tot += __shfl_xor(tot, 2);
+    tot += __shfl_xor(tot, 1);
+    if ((lane & 3) == 0) part[wave][((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1)] = tot;
     __syncthreads();
     if (tid < kF32wRows * NT) {
         const int r = tid / NT, t = tid % NT;
@@ -84,117 +98,48 @@ __global__ void __launch_bounds__(256) linear_f32w_kernel(const TX *x, const flo
     }
 }
 
-// ---------------- top-k router ----------------
-// One wave64 per token. The E logits stay in registers (lane l holds experts l, l + 64, ...); a pick is a wave-wide
-// maximum of 64-bit keys (value bits made monotone in the high word, ~index in the low word), so the larger logit
-// wins and a tie goes to the lower index (kernels/moe_router.hpp:11-13) with one integer compare. Only the lane whose
-// expert was picked rescans its registers. Then the softmax over the k picks.
-__device__ __forceinline__ uint64_t route_key(float v, int idx) {
-    const uint32_t b = v == 0.f ? 0u : __float_as_uint(v);  // -0 ties +0, as a float compare does
-    const uint32_t hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((uint64_t)hi << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
+template <typename TX, int NT>
+__global__ void __launch_bounds__(256) linear_f32w_kernel(const TX *x, const float *W, float *y, int64_t M, int64_t N,
+                                                          int64_t K) {
+    __shared__ float part[4][kF32wRows * NT];
+    project_rows<TX, NT>(x, W, y, M, N, K, part);
 }
 
-// The logit a key was made from (a -0 logit comes back as +0, which no later use tells apart).
-__device__ __forceinline__ float key_value(uint64_t key) {
-    const uint32_t hi = (uint32_t)(key >> 32);
-    return __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
-}
-
-// Wave-wide maximum of 64-bit keys. Within a row of 16 lanes the partners come through DPP (quad [1,0,3,2],
-// quad [2,3,0,1], half-row mirror, row mirror: after each step every lane holds the maximum over 2, 4, 8, 16 lanes,
-// since max needs no particular pairing); across the four rows two LDS-routed shuffles.
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_max(uint64_t k) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, 0xF, 0xF, false);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    return o > k ? o : k;
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-    k = dpp_max<0xB1>(k);   // quad_perm [1,0,3,2]
-    k = dpp_max<0x4E>(k);   // quad_perm [2,3,0,1]
-    k = dpp_max<0x141>(k);  // row_half_mirror
-    k = dpp_max<0x140>(k);  // row_mirror
-#pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)k, off), hi = __shfl_xor((uint32_t)(k >> 32), off);
-        const uint64_t o = ((uint64_t)hi << 32) | lo;
-        k = o > k ? o : k;
-    }
-    return k;
-}
-
+// ---------------- top-k router: one wave a token (routing::route_token) ----------------
 template <typename T, int NV>
 __global__ void __launch_bounds__(64) moe_router_kernel(const T *logits, int64_t ld, int E, int k, const T *shared,
                                                         int64_t shared_ld, int32_t shared_id, int32_t *ids,
                                                         float *coef, int A, uint32_t *err) {
     const int64_t m = blockIdx.x;
-    const int lane = threadIdx.x;
     const T *row = logits + m * ld;
-    float v[NV];
-    int bad = INT_MAX;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int e = lane + 64 * j;
-        const float xv = e < E ? load_act(row, e) : -INFINITY;
-        v[j] = xv;
-        if (e < E && !isfinite(xv) && e < bad) bad = e;
+    const float sl = shared != nullptr ? load_act(shared, m * shared_ld) : 0.f;
+    routing::route_token<NV>([&](int e) { return load_act(row, e); }, E, k, shared != nullptr, sl, shared_id, m,
+                             ids + m * A, coef + m * A, nullptr, err);
+}
+
+// ---------------- top-k routing + grouping in one block (verify width) ----------------
+// moe_router and moe_group_routes fused where one block can hold the slots: 16 waves route 16 tokens at a time
+// (routing::route_token), the ids also land in LDS, then the 1024 threads counting-sort the slots into the
+// workspace (routing::group_in_block). One launch and no global round trip between the two.
+constexpr int kRgThreads = 1024, kRgMaxSlots = 2048;
+
+template <typename T, int NV>
+__global__ void __launch_bounds__(kRgThreads)
+    router_group_kernel(const T *logits, int64_t ld, int M, int E, int k, int32_t *ids, float *coef,
+                        uint32_t *router_err, int32_t *ws, int Tmax, int WTmax, uint32_t *expert_err) {
+    __shared__ int32_t lds_ids[kRgMaxSlots];
+    __shared__ int cnt[kRgThreads], cursor[kRgThreads];
+    __shared__ int wtot[kRgThreads / 64][3];
+    __shared__ int first_bad;
+    const int wave = threadIdx.x >> 6;
+    for (int m = wave; m < M; m += kRgThreads / 64) {
+        const T *row = logits + (int64_t)m * ld;
+        routing::route_token<NV>([&](int e) { return load_act(row, e); }, E, k, false, 0.f, 0, m,
+                                 ids + (int64_t)m * k, coef + (int64_t)m * k, lds_ids + m * k, router_err);
     }
-    float sl = 0.f;
-    if (shared != nullptr) {
-        sl = load_act(shared, m * shared_ld);
-        if (!isfinite(sl) && E < bad) bad = E;
-    }
-    for (int off = 32; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off));
-    int32_t *id_row = ids + m * A;
-    float *coef_row = coef + m * A;
-    if (bad != INT_MAX) {  // a non-finite logit fails the token (moe_router.hpp:19-23)
-        if (lane == 0) flag_error(err, (uint32_t)m, (uint32_t)bad);
-        for (int a = lane; a < A; a += 64) id_row[a] = -1, coef_row[a] = qnan();
-        return;
-    }
-    // Padding past E must never win: its key is below every finite logit's.
-    auto lane_best = [&]() {
-        uint64_t b = 0;
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int e = lane + 64 * j;
-            const uint64_t key = e < E ? route_key(v[j], e) : 0;
-            b = key > b ? key : b;
-        }
-        return b;
-    };
-    uint64_t mine = lane_best();
-    float my_v = -INFINITY, top = 0.f;
-    int my_i = -1;
-    for (int r = 0; r < k; ++r) {
-        const uint64_t best = wave_max_u64(mine);
-        const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
-        const float bv = key_value(best);
-        if (r == 0) top = bv;
-        if (lane == r) my_v = bv, my_i = bi;
-        if ((bi & 63) == lane) {  // the picked expert is this lane's
-#pragma unroll
-            for (int j = 0; j < NV; ++j)
-                if (lane + 64 * j == bi) v[j] = -INFINITY;
-            mine = 0;
-#pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int e = lane + 64 * j;
-                if (e < E && v[j] != -INFINITY) {
-                    const uint64_t key = route_key(v[j], e);
-                    mine = key > mine ? key : mine;
-                }
-            }
-        }
-    }
-    const float ex = lane < k ? expf(my_v - top) : 0.f;
-    float sum = ex;
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    if (lane < k) id_row[lane] = my_i, coef_row[lane] = ex / sum;
-    if (shared != nullptr && lane == 0) id_row[k] = shared_id, coef_row[k] = 1.0f / (1.0f + expf(-sl));
+    __syncthreads();
+    routing::group_in_block<kRgThreads>([&](int s) { return lds_ids[s]; }, M * k, E, Tmax, WTmax, ws, expert_err,
+                                        cnt, cursor, wtot, &first_bad);
 }
 
 }  // namespace
@@ -255,6 +200,39 @@ int sx_moe_router(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t 
     if (act == SX_ACT_F32) by_nv(float{});
     else by_nv(uint16_t{});
     SX_LAUNCHED("moe_router M=", M, " E=", E, " k=", k);
+    return SX_OK;
+}
+
+int sx_moe_router_group(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int act, int32_t *ids,
+                        float *coef, uint32_t *router_err, void *ws, size_t ws_bytes, uint32_t *expert_err,
+                        sx_stream stream) {
+    SX_CHECK(logits != nullptr && ids != nullptr && coef != nullptr && router_err != nullptr && ws != nullptr &&
+                 expert_err != nullptr,
+             "null pointer");
+    SX_CHECK(M >= 1 && E >= 1 && E <= 1023 && k >= 1 && k <= E && k <= 32 && M * k <= kRgMaxSlots, "M = ", M,
+             ", E = ", E, ", k = ", k, " (E <= 1023, k <= min(E, 32), M*k <= ", kRgMaxSlots,
+             "; larger: moe_router + moe_group_routes)");
+    SX_CHECK(ld >= E, "logits row stride ld = ", ld, " < E = ", E);
+    SX_CHECK((const void *)ids != (const void *)coef, "ids and coef are the same buffer");
+    SX_CHECK(act == SX_ACT_F32 || act == SX_ACT_BF16, "unsupported activation dtype ", act);
+    SX_CHECK(aligned(ws, 4), "workspace must be 4-byte aligned");
+    const Layout L = layout_of(M, k, E);
+    SX_CHECK(ws_bytes >= (size_t)L.ints() * 4, "workspace of ", ws_bytes, " bytes, needs ", L.ints() * 4);
+    const int nv = E <= 256 ? 4 : E <= 512 ? 8 : 16;
+    auto go = [&](auto tag, auto nvc) {
+        using T = decltype(tag);
+        router_group_kernel<T, decltype(nvc)::value><<<1, kRgThreads, 0, stream_of(stream)>>>(
+            static_cast<const T *>(logits), ld, (int)M, (int)E, (int)k, ids, coef, router_err,
+            static_cast<int32_t *>(ws), (int)L.Tmax, (int)L.WTmax, expert_err);
+    };
+    auto by_nv = [&](auto tag) {
+        if (nv == 4) go(tag, std::integral_constant<int, 4>{});
+        else if (nv == 8) go(tag, std::integral_constant<int, 8>{});
+        else go(tag, std::integral_constant<int, 16>{});
+    };
+    if (act == SX_ACT_F32) by_nv(float{});
+    else by_nv(uint16_t{});
+    SX_LAUNCHED("moe_router_group M=", M, " E=", E, " k=", k);
     return SX_OK;
 }
 

@@ -112,6 +112,20 @@ def route_workspace_bytes(M, A, E):
     return n.value
 
 
+def router_group(logits, E, k, ws=None, ids=None, coef=None, router_err=None, expert_err=None, stream=None):
+    """moe_router + moe_group_routes in one launch (M * k <= 2048)."""
+    M, ld = logits.shape
+    dev = logits.device
+    ws = torch.empty(route_workspace_bytes(M, k, E) // 4, dtype=torch.int32, device=dev) if ws is None else ws
+    ids = torch.empty((M, k), dtype=torch.int32, device=dev) if ids is None else ids
+    coef = torch.empty((M, k), dtype=torch.float32, device=dev) if coef is None else coef
+    router_err = _err(dev) if router_err is None else router_err
+    expert_err = _err(dev) if expert_err is None else expert_err
+    check(lib().sx_moe_router_group(_p(logits), ld, M, E, k, act_of(logits), _p(ids), _p(coef), _p(router_err),
+                                    _p(ws), ws.numel() * 4, _p(expert_err), _s(stream)))
+    return ids, coef, ws, router_err, expert_err
+
+
 def group_routes(ids, E, ws=None, err=None, stream=None):
     M, A = ids.shape
     nb = route_workspace_bytes(M, A, E)

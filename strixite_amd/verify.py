@@ -9,7 +9,8 @@ from . import kernels as kx
 
 
 class MoeVerifyLayer:
-    """One MoE FFN sublayer: router projection -> moe_router (top-k, softmax) -> moe_group_routes -> grouped
+    """One MoE FFN sublayer: router projection -> moe_router (top-k, softmax) + moe_group_routes (one launch at
+    verify width) -> grouped
     gate_up with the SwiGLU epilogue -> grouped down + combine. Weights: Wr FP32 [E, d], gate_up q4 [E * 2I, d],
     down q4 [E * d, I] (experts stacked, runtime/qwen4exp.cpp:126-129)."""
 
@@ -34,11 +35,15 @@ class MoeVerifyLayer:
     def forward(self, x, stream=None):
         M = x.shape[0]
         assert M <= self.M
-        kx.linear_f32w(x, self.Wr, y=self.logits[:M], stream=stream)
-        kx.moe_router(self.logits[:M], self.E, self.k, ids=self.ids[:M], coef=self.coef[:M], err=self.router_err,
-                      stream=stream)
         ws = self.ws if M == self.M else self.ws[:kx.route_workspace_bytes(M, self.k, self.E) // 4]
-        kx.group_routes(self.ids[:M], self.E, ws=ws, err=self.expert_err, stream=stream)
+        kx.linear_f32w(x, self.Wr, y=self.logits[:M], stream=stream)
+        if M * self.k <= 2048:  # top-k + grouping in one launch
+            kx.router_group(self.logits[:M], self.E, self.k, ws=ws, ids=self.ids[:M], coef=self.coef[:M],
+                            router_err=self.router_err, expert_err=self.expert_err, stream=stream)
+        else:
+            kx.moe_router(self.logits[:M], self.E, self.k, ids=self.ids[:M], coef=self.coef[:M],
+                          err=self.router_err, stream=stream)
+            kx.group_routes(self.ids[:M], self.E, ws=ws, err=self.expert_err, stream=stream)
         kx.gather_grouped(x, self.gate_up, self.E, ws, M, self.k, swiglu=True, y=self.h[:M], stream=stream)
         kx.combine_grouped(self.h[:M], self.down, self.E, self.ids[:M], self.coef[:M], ws,
                            partial=self.partial[:M * self.k], y=self.y[:M], math=MOE_F32, stream=stream)

@@ -93,6 +93,49 @@ def test_group_routes_invariants():
     assert list(err.cpu().numpy()[:3]) == [1, -1, 53]
 
 
+def _ws_parts(w, S, E):
+    """The defined parts of a route workspace (tile arrays past n_tiles / n_wtiles are never written)."""
+    Tmax, WTmax = S // 16 + E + 2, S // 64 + E + 2
+    o = 4 + E + 2
+    t = o + S
+    n, nw = w[0], w[3]
+    tiles = np.concatenate([w[t:t + n], w[t + Tmax:t + Tmax + n], w[t + 2 * Tmax:t + 2 * Tmax + nw],
+                            w[t + 2 * Tmax + WTmax:t + 2 * Tmax + WTmax + nw]])
+    return {"head": w[:4], "off": w[4:o], "slots": w[o:o + S], "tiles": tiles}
+
+
+@pytest.mark.parametrize("M,E,k,act", [(6, 512, 10, orc.F32), (1, 512, 10, orc.F32), (17, 64, 32, orc.BF16),
+                                       (64, 1000, 8, orc.F32), (33, 130, 7, orc.BF16)])
+def test_router_group_matches_two_calls(M, E, k, act):
+    """One launch == moe_router + moe_group_routes: ids and coefficients bit for bit, the workspace's header, offsets
+    and tiles equal, each bucket's slots the same set, and ids exact against the oracle; a non-finite row fails its
+    token in both."""
+    import torch
+    rng = np.random.default_rng(M * 7 + E)
+    L = rng.standard_normal((M, E)).astype(np.float32)
+    L[0, [1, E // 2]] = 5.0  # a tie: lower index first
+    if M > 3:
+        L[3, E - 1] = np.nan
+    Ld = util.f32_dev(L) if act == orc.F32 else util.bf16_dev(util.f32_to_bf16(L))
+    ids2, coef2, rerr2 = kx().moe_router(Ld, E, k)
+    ws2, eerr2 = kx().group_routes(ids2, E)
+    ids, coef, ws, rerr, eerr = kx().router_group(Ld, E, k)
+    sync()
+    assert np.array_equal(ids.cpu().numpy(), ids2.cpu().numpy())
+    assert np.array_equal(coef.cpu().numpy().view(np.uint32), coef2.cpu().numpy().view(np.uint32))
+    assert np.array_equal(rerr.cpu().numpy(), rerr2.cpu().numpy())
+    assert np.array_equal(eerr.cpu().numpy(), eerr2.cpu().numpy())
+    a, b = _ws_parts(ws.cpu().numpy(), M * k, E), _ws_parts(ws2.cpu().numpy(), M * k, E)
+    for key in ("head", "off", "tiles"):
+        assert np.array_equal(a[key], b[key]), key
+    off = a["off"]
+    for e in range(E + 1):
+        assert sorted(a["slots"][off[e]:off[e + 1]]) == sorted(b["slots"][off[e]:off[e + 1]])
+    Lh = L if act == orc.F32 else util.bf16_to_f32(util.f32_to_bf16(L))
+    ref_ids, _, _ = orc.moe_router(Lh, E, k)
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+
+
 # ---------------- experts ----------------
 
 def make_experts(seed, E, I, d, G=128):
