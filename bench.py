@@ -190,6 +190,65 @@ def cpu_baseline(layer, xs, budget_s):
                       f"FP64 accumulation, {threads} threads"}
 
 
+def prefill_layer(steps=20):
+    """x BF16 [2048, 4096] through the router projection, the Zipf bias, top-10 routing, grouping,
+    the grouped gate_up + SwiGLU and down + combine (q4 G = 128 experts, MFMA 64-slot x 128-row tiles)."""
+    import torch
+
+    from strixite_amd import kernels as kx
+    from strixite_amd import synthetic as syn
+
+    E, d, I, k, M = 512, 4096, 1024, 10, 2048
+    Wr = syn.router_weight(E, d, seed=61)
+    gu = syn.qweight(4, E * 2 * I, d, 128, seed=62)
+    dn = syn.qweight(4, E * d, I, 128, seed=63)
+    bias = syn.zipf_router_bias(E, seed=64)
+    xs = [syn.activations(M, d, seed=65 + r) for r in range(2)]
+    logits = torch.empty((M, E), dtype=torch.float32, device="cuda")
+    ids = torch.empty((M, k), dtype=torch.int32, device="cuda")
+    coef = torch.empty((M, k), dtype=torch.float32, device="cuda")
+    ws = torch.empty(kx.route_workspace_bytes(M, k, E) // 4, dtype=torch.int32, device="cuda")
+    h = torch.empty((M, k, I), dtype=torch.bfloat16, device="cuda")
+    part = torch.empty((M * k, d), dtype=torch.float32, device="cuda")
+    y = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
+    rerr, eerr = torch.zeros(4, dtype=torch.int32, device="cuda"), torch.zeros(4, dtype=torch.int32, device="cuda")
+    stamps = {}
+
+    def layer(i, mark=False):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if mark else None
+        x = xs[i % 2]
+        if mark:
+            ev[0].record()
+        kx.linear_f32w(x, Wr, y=logits)
+        logits.add_(bias)
+        kx.moe_router(logits, E, k, ids=ids, coef=coef, err=rerr)
+        kx.group_routes(ids, E, ws=ws, err=eerr)
+        if mark:
+            ev[1].record()
+        kx.gather_grouped(x, gu, E, ws, M, k, swiglu=True, y=h)
+        if mark:
+            ev[2].record()
+        kx.combine_grouped(h, dn, E, ids, coef, ws, partial=part, y=y)
+        if mark:
+            ev[3].record()
+            stamps[i] = ev
+
+    ms = time_launches(layer, steps, warm=3)
+    layer(0, mark=True)
+    torch.cuda.synchronize()
+    ev = stamps[0]
+    t_route, t_gu, t_dn = (ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2]), ev[2].elapsed_time(ev[3]))
+    counts = torch.bincount(ids.flatten(), minlength=E)
+    U = int((counts > 0).sum())
+    flops = 2.0 * M * k * (2 * I * d + d * I)
+    wbytes = U * (gu.nbytes() + dn.nbytes()) // E
+    return {"us": round(ms * 1e3, 1), "prefill_tok_per_s": round(M / (ms * 1e-3), 1),
+            "mfma_frac": round(flops / (ms * 1e-3) / 2.5e15, 4), "expert_weight_GBps": round(wbytes / (ms * 1e-3) / 1e9, 1),
+            "routing_us": round(t_route * 1e3, 1), "gate_up_us": round(t_gu * 1e3, 1), "down_combine_us": round(t_dn * 1e3, 1),
+            "gate_up_mfma_frac": round(2.0 * M * k * 2 * I * d / (t_gu * 1e-3) / 2.5e15, 4),
+            "distinct_experts": U, "max_bucket": int(counts.max()), "flops": flops}
+
+
 def extra_configs(out):
     import torch
 
@@ -210,6 +269,8 @@ def extra_configs(out):
         res[name] = {"us": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                      "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del reps
+    # config 4: the MoE layer at prefill width, M = 2048, Zipf-skewed routing; grouped MFMA experts
+    res["cfg4_prefill_layer"] = prefill_layer()
     # config 5: q8 LM head 151936 x 4096 at M = 6 -> top-40 -> sampled acceptance of 5 drafts
     V, d = 151936, 4096
     w = syn.qweight(8, V, d, 64, seed=50)

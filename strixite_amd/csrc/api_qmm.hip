@@ -6,6 +6,7 @@
 #include <vector>
 #include <cstdio>
 #include <map>
+#include "gemm_grouped.hpp"
 #include "qmm.hpp"
 
 #include <cstdlib>
@@ -265,6 +266,10 @@ int sx_linear_q4_experts_gather_grouped(const void *x, const sx_qview *w, int64_
     if (int rc = grouped_common(fn, x, w, E, M, A, ws, ws_bytes, y, act, math)) return rc;
     const int64_t N = w->N / E, es = act_bytes(act), S = M * A;
     SX_CHECK(apart(x, M * w->K * es, y, S * N * es), fn, " y overlaps x");
+    if (M >= gg::kPrefillMinTokens && gg::eligible(4, w->G, w->K, act) && aligned(w->scale, 4) && aligned(w->minv, 4)) {
+        SX_HIP(gg::launch(qmm::GATHER, x, w, y, static_cast<const int32_t *>(ws), M, A, E, act, stream_of(stream)), fn);
+        return SX_OK;
+    }
     Params p{};
     p.x = x, p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.y = y, p.ws = static_cast<const int32_t *>(ws);
     p.M = M, p.A = A, p.E = E, p.N = N, p.K = w->K, p.G = (int)w->G;
@@ -281,6 +286,10 @@ int sx_linear_q4_experts_gather_swiglu_grouped(const void *x, const sx_qview *w,
     const int64_t N = w->N / E, es = act_bytes(act), S = M * A;
     SX_CHECK(N % 2 == 0, fn, " SwiGLU gather needs an even row count per expert ([gate | up]), got ", N);
     SX_CHECK(apart(x, M * w->K * es, h, S * (N / 2) * es), fn, " h overlaps x");
+    if (M >= gg::kPrefillMinTokens && gg::eligible(4, w->G, w->K, act) && aligned(w->scale, 4) && aligned(w->minv, 4)) {
+        SX_HIP(gg::launch(qmm::SWIGLU, x, w, h, static_cast<const int32_t *>(ws), M, A, E, act, stream_of(stream)), fn);
+        return SX_OK;
+    }
     Params p{};
     p.x = x, p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.y = h, p.ws = static_cast<const int32_t *>(ws);
     p.M = M, p.A = A, p.E = E, p.N = N, p.K = w->K, p.G = (int)w->G;
@@ -300,6 +309,11 @@ int sx_linear_q4_experts_combine_grouped(const void *h, const sx_qview *w, int64
     SX_CHECK(apart(y, M * N * es, h, S * w->K * es), fn, " y overlaps h");
     SX_CHECK(apart(y, M * N * es, partial, S * N * 4), fn, " y overlaps partial");
     SX_CHECK(apart(partial, S * N * 4, h, S * w->K * es), fn, " partial overlaps h");
+    if (M >= gg::kPrefillMinTokens && gg::eligible(4, w->G, w->K, act) && aligned(w->scale, 4) && aligned(w->minv, 4)) {
+        SX_HIP(gg::launch(qmm::COMBINE, h, w, partial, static_cast<const int32_t *>(ws), M, A, E, SX_ACT_F32,
+                          stream_of(stream)), fn);
+        return combine_reduce(partial, ids, coef, M, A, E, N, y, act, stream_of(stream));
+    }
     Params p{};
     p.x = h, p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.y = partial, p.ws = static_cast<const int32_t *>(ws);
     p.M = M, p.A = A, p.E = E, p.N = N, p.K = w->K, p.G = (int)w->G;

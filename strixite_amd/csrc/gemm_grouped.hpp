@@ -1,0 +1,16 @@
+// Prefill-width grouped expert GEMM (q4 G = 128 experts, BF16 activations) on the matrix cores.
+#pragma once
+#include "qmm.hpp"
+
+namespace sx::gg {
+
+// Tokens from which the grouped entry points take this kernel (the reference switches its grouped path to the WMMA
+// tiles at prefill width; at verify width buckets hold a few slots and qmm's one pass over the weights wins).
+constexpr int64_t kPrefillMinTokens = 32;
+
+bool eligible(int bits, int64_t G, int64_t K, int act);
+// mode: qmm::SWIGLU (h [S, N/2]), qmm::GATHER (y [S, N]), qmm::COMBINE (FP32 partials [S, N]); N = w->N / E.
+hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int32_t *ws, int64_t M, int64_t A,
+                  int64_t E, int out_act, hipStream_t stream);
+
+}  // namespace sx::gg

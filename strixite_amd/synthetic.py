@@ -32,6 +32,17 @@ def router_weight(E, K, seed, device="cuda"):
     return torch.randn(E, K, device=device, generator=g) * 0.02
 
 
+def zipf_router_bias(E, seed, s=1.1, scale=0.3, device="cuda"):
+    """BASELINE config 4's routing skew: a bias added to the router logits, -scale * s * ln(rank + 1) for the
+    experts in a seeded random order of ranks (a Zipf(s) prior in log space). scale = 0.3 against logits of standard
+    deviation ~1.3 (x ~ N(0, 1), Wr ~ N(0, 0.02), d = 4096) gives buckets of 0..~450 of 20,480 slots at top-10."""
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(E, generator=g)
+    bias = torch.empty(E, dtype=torch.float32)
+    bias[perm] = -scale * s * torch.log(torch.arange(E, dtype=torch.float32) + 1.0)
+    return bias.to(device)
+
+
 def host_rows(w, r0, r1):
     """Host numpy copy (q, scale, minv) of weight rows [r0, r1): for the oracle on the rows a test touches."""
     r0, r1 = int(r0), int(r1)  # numpy integers would overflow int32 on the byte offsets of large weights

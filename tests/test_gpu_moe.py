@@ -210,6 +210,37 @@ def test_grouped_matches_per_slot_oracle(M, A, E, I, d):
     assert err.cpu().numpy()[0] == 0
 
 
+@pytest.mark.parametrize("M,A,E,I,d", [(96, 4, 8, 256, 512), (40, 3, 5, 128, 256), (64, 2, 3, 384, 1024)])
+def test_prefill_grouped_mfma_matches_oracle(M, A, E, I, d):
+    """Prefill width (M >= 32 takes the 64-slot x 128-row MFMA kernel): gather, SwiGLU gather and combine against the
+    oracle, with one bucket far over 64 slots (several wide tiles), one of exactly 64, and an invalid id (NaN rows,
+    error words from the grouping)."""
+    import torch
+    wgu, wdn, rng = make_experts(M * 31 + E, E, I, d)
+    x = util.f32_to_bf16(rng.standard_normal((M, d)).astype(np.float32))
+    ids = np.stack([rng.choice(E, A, replace=False) for _ in range(M)]).astype(np.int32)
+    ids[: M // 2, 0] = 1                       # bucket 1: >= M/2 slots
+    if M >= 64:
+        ids[:, A - 1] = np.where(np.arange(M) < 64, 2, ids[:, A - 1])  # bucket 2 gets 64 more (duplicates allowed)
+    ids[5, A - 1] = -1                         # an invalid slot
+    coef = rng.random((M, A)).astype(np.float32)
+    ids_d = torch.from_numpy(ids).cuda()
+    Wgu, Wdn = kx().QWeight.upload(wgu), kx().QWeight.upload(wdn)
+    xd = util.bf16_dev(x)
+    ws, err = kx().group_routes(ids_d, E)
+    gu = kx().gather_grouped(xd, Wgu, E, ws, M, A)
+    h = kx().gather_grouped(xd, Wgu, E, ws, M, A, swiglu=True)
+    y = kx().combine_grouped(h, Wdn, E, ids_d, util.f32_dev(coef), ws)
+    sync()
+    ref_gu, _ = orc.experts_gather(x, wgu, E, ids)
+    ref_h, _ = orc.experts_gather(x, wgu, E, ids, swiglu=True)
+    util.assert_close(util.host_bits(gu), ref_gu, what="prefill gather_grouped")
+    util.assert_close(util.host_bits(h), ref_h, what="prefill gather_swiglu_grouped")
+    ref_y, _ = orc.experts_combine(util.host_bits(h), wdn, E, ids, coef)
+    util.assert_close(util.host_bits(y), ref_y, what="prefill combine_grouped")
+    assert list(err.cpu().numpy()[:3]) == [1, -1, 5 * A + A - 1]
+
+
 def test_grouped_bad_id_rows_are_nan():
     import torch
     M, A, E, I, d = 3, 2, 4, 32, 128
