@@ -3,11 +3,12 @@
 // The verify kernel (qmm) stages every activation row of a unit over the whole K in LDS and passes the weights once
 // per 16 rows; with hundreds of rows a bucket (kernels/moe_grouped.hpp:5-17: the prefill path) that re-streams each
 // expert's weights per 16 rows. Here a block owns a 64-slot tile of one bucket (the workspace's wide tiles,
-// moe_grouped.hip:63-81) times 128 weight rows (4 waves x 2 tiles of 16), and walks K in blocks of 2 spans (256
-// codes): the activation rows of the block go through LDS, double-buffered, while each wave's weight codes load
-// straight into the MFMA B layout (16 rows x 64 B a load, as in qmm) and feed 4 token blocks of 16 slots each, so a
-// code fragment is reused 4 times and each weight tile is read once a 64-slot tile (the other tiles of the same
-// bucket run next to it and find it in L2). Per span (one quantization group):
+// moe_grouped.hip:63-81) times 256 weight rows (8 waves x 2 tiles of 16; SwiGLU: 128 features, gate and up), and
+// walks K in blocks of 2 spans (256 codes) through a 3-stage pipeline: the block's activation rows go to LDS by
+// direct global->LDS loads ([chunk][row] 16-byte units, so the MFMA reads are conflict-free), two blocks ahead,
+// while each wave's weight codes load straight into the MFMA B layout (16 rows x 64 B a load, as in qmm) and feed
+// 4 token blocks of 16 slots each: a code fragment is used 4 times and each weight tile is read once a 64-slot tile
+// (the other tiles of the same bucket run next to it and find it in L2). Per span (one quantization group):
 //   acc[token][row] += s[row] * D + (m[row] - 128 s[row]) * sum_span x[token]
 // with D = sum x * (128 + code) exactly from v_mfma_f32_16x16x32_bf16 (the same identity as qmm).
 // Epilogues: SwiGLU (gate and up tiles of the same 16 features in one wave), plain gather, FP32 partials (combine).
@@ -20,14 +21,17 @@ namespace {
 using qmm::detail::bf16x8;
 using qmm::detail::f32x4;
 
-constexpr int kThreads = 256, kWaves = 4;
+constexpr int kThreads = 512, kWaves = 8;
 constexpr int kBM = 64;                      // slots a block tile
 constexpr int kSpan = 128, kSpanBytes = 64;  // q4 codes / bytes a span (= one G = 128 group)
 constexpr int kBKS = 2;                      // spans a K block
 constexpr int kBK = kBKS * kSpan;            // codes a K block
-constexpr int kLdx = kBK + 8;                // LDS row stride (BF16): +16 B staggers the rows over the banks
+constexpr int kChunks = kBK / 8;             // 16-byte chunks of a row a K block (32): 4 a wave
+constexpr int kStages = 3;                   // K blocks in LDS: two in flight while one is computed
 constexpr int kTW = 2;                       // 16-row weight tiles a wave
-constexpr int kXLoads = kBM * (kBK / 8) / kThreads;  // 16-byte activation loads a thread a K block (8)
+constexpr size_t kStageBytes = (size_t)kChunks * kBM * 16;  // [chunk][row] 16-byte units: 32 KB
+constexpr size_t kSumBytes = (size_t)kBKS * kBM * 4;         // [span][row] FP32
+constexpr int kLoadsPerIssue = kChunks / kWaves + kTW * kBKS + 2 * kTW;  // VMEM instructions a wave a K block
 
 struct Params {
     const uint16_t *x;  // BF16 activations [tokens or slots, K]
@@ -39,13 +43,24 @@ struct Params {
     int64_t E;
 };
 
-size_t lds_bytes() { return (size_t)2 * kBM * kLdx * 2 + (size_t)2 * kBKS * kBM * 4; }
+
+// B operand of MFMA c from a lane's 16 code bytes in natural code order: dword c's nibbles j = 0..7 (codes
+// k0 + j, the low nibble the even code) as BF16 128 + code, pairs assembled by byte selects.
+__device__ __forceinline__ bf16x8 codes_nat(const uint4 &w, int c) {
+    const uint32_t d = qmm::detail::dword(w, c), lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+    uint4 v;
+    v.x = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x43004300u;
+    v.y = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x43004300u;
+    v.z = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x43004300u;
+    v.w = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x43004300u;
+    return __builtin_bit_cast(bf16x8, v);
+}
 
 template <int MODE, typename TY>
 __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    uint16_t *xs = reinterpret_cast<uint16_t *>(smem);                         // [2][kBM][kLdx] code order
-    float *xsum = reinterpret_cast<float *>(smem + (size_t)2 * kBM * kLdx * 2);  // [2][kBKS][kBM]
+    // One array a stage, so that the wait-count pass tells a stage's LDS DMA apart from the others'.
+    __shared__ __attribute__((aligned(16))) unsigned char xs0[kStageBytes], xs1[kStageBytes], xs2[kStageBytes];
+    __shared__ __attribute__((aligned(16))) float ss[kStages][kBKS * kBM];
     __shared__ int64_t s_xrow[kBM], s_out[kBM];
     __shared__ int s_T, s_bucket;
 
@@ -110,19 +125,26 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
         srow[t] = reinterpret_cast<const uint32_t *>(p.scale + row * ngroups);
         mrow[t] = reinterpret_cast<const uint32_t *>(p.minv + row * ngroups);
     }
+    // the activation row this lane stages (rows past T repeat row T - 1; their outputs are never stored)
+    const uint16_t *xlane = p.x + s_xrow[min(lane, T - 1)];
 
-    // ---- the pipeline: K block kb's loads go out while kb - 1 is computed ----
+    // ---- the pipeline: K block kb + 2 is loading while kb is summed and computed ----
     const int nkb = (int)(K / kBK);
-    uint4 wq[2][kTW][kBKS];
-    uint32_t wsc[2][kTW], wmn[2][kTW];
-    uint4 xr[kXLoads];
-    auto issue = [&](int kb, auto slot_tag) {  // kb past the end re-loads the last block (never used)
+    uint4 wq[kStages][kTW][kBKS];
+    uint32_t wsc[kStages][kTW], wmn[kStages][kTW];
+    auto stage_at = [&](int st) -> unsigned char * { return st == 0 ? xs0 : st == 1 ? xs1 : xs2; };
+    auto sums_at = [&](int st) -> float * { return ss[st]; };
+    // K block kb (clamped: past the end it re-loads the last block, never used): this wave's 4 activation chunks of
+    // all 64 rows straight into LDS ([chunk][row], lane = row), then its weight codes, scales and mins into registers.
+    auto issue = [&](int kb, int st, auto slot_tag) {
         constexpr int R = decltype(slot_tag)::value;
         const int k = min(kb, nkb - 1);
 #pragma unroll
-        for (int b = 0; b < kXLoads; ++b) {
-            const int i = b * kThreads + tid, r = min(i >> 5, T - 1), c8 = i & 31;  // rows past T repeat row T - 1
-            xr[b] = *reinterpret_cast<const uint4 *>(p.x + s_xrow[r] + (int64_t)k * kBK + c8 * 8);
+        for (int i = 0; i < kChunks / kWaves; ++i) {
+            const int c = wave * (kChunks / kWaves) + i;
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(xlane + (int64_t)k * kBK + c * 8),
+                (__attribute__((address_space(3))) void *)(stage_at(st) + (size_t)c * kBM * 16), 16, 0, 0);
         }
 #pragma unroll
         for (int t = 0; t < kTW; ++t) {
@@ -132,19 +154,20 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
             wsc[R][t] = srow[t][k], wmn[R][t] = mrow[t][k];
         }
     };
-    auto stage = [&](int buf) {  // the activation registers of one K block -> LDS (code order) + per-span sums
-        uint16_t *xb = xs + (size_t)buf * kBM * kLdx;
-        float *sb = xsum + (size_t)buf * kBKS * kBM;
+    // Span sums of the staged rows: 4 threads a (span, row), 32 codes each, added across the quad.
+    auto sum_spans = [&](int st) {
+        const int q = tid >> 2, part = tid & 3, s = q >> 6, r = q & (kBM - 1);
+        const unsigned char *xb = stage_at(st);
+        float sum = 0.f;
 #pragma unroll
-        for (int b = 0; b < kXLoads; ++b) {
-            const int i = b * kThreads + tid, r = i >> 5, c8 = i & 31;
-            uint4 planes[1];
-            float sum;
-            qmm::detail::chunk_planes<4, 1, uint16_t>(xr[b], planes, sum);
-            *reinterpret_cast<uint4 *>(xb + r * kLdx + c8 * 8) = planes[0];
-            sum = qmm::detail::group_sum_c<16>(sum);  // 16 chunks of 8 = one span
-            if ((c8 & 15) == 0) sb[(c8 >> 4) * kBM + r] = sum;
+        for (int i = 0; i < 4; ++i) {
+            float v[8];
+            qmm::detail::unpack8(*reinterpret_cast<const uint4 *>(xb + ((size_t)(s * 16 + part * 4 + i) * kBM + r) * 16), v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sum += v[j];
         }
+        sum = qmm::detail::group_sum_c<4>(sum);
+        if (part == 0) sums_at(st)[s * kBM + r] = sum;
     };
 
     f32x4 acc[kTW][4];
@@ -153,10 +176,10 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) acc[t][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](int buf, auto slot_tag) {
+    auto compute = [&](int st, auto slot_tag) {
         constexpr int R = decltype(slot_tag)::value;
-        const uint16_t *xb = xs + (size_t)buf * kBM * kLdx;
-        const float *sb = xsum + (size_t)buf * kBKS * kBM;
+        const unsigned char *xb = stage_at(st);
+        const float *sb = sums_at(st);
 #pragma unroll
         for (int s = 0; s < kBKS; ++s) {
             bf16x8 B[kTW][4];
@@ -164,7 +187,7 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
 #pragma unroll
             for (int t = 0; t < kTW; ++t) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) B[t][c] = qmm::detail::codes_b<4>(wq[R][t][s], c);
+                for (int c = 0; c < 4; ++c) B[t][c] = codes_nat(wq[R][t][s], c);
                 const uint32_t sw = wsc[R][t], mw = wmn[R][t];
                 sc[t] = __uint_as_float(s ? (sw & 0xFFFF0000u) : (sw << 16));
                 const float mv = __uint_as_float(s ? (mw & 0xFFFF0000u) : (mw << 16));
@@ -173,9 +196,9 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
                 bf16x8 Aop[4];
-                const uint16_t *xa = xb + (tb * 16 + n16) * kLdx + s * kSpan + g * 32;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) Aop[c] = *reinterpret_cast<const bf16x8 *>(xa + c * 8);
+                for (int c = 0; c < 4; ++c)
+                    Aop[c] = *reinterpret_cast<const bf16x8 *>(xb + ((size_t)(s * 16 + g * 4 + c) * kBM + tb * 16 + n16) * 16);
                 const float4 xv = *reinterpret_cast<const float4 *>(sb + s * kBM + tb * 16 + 4 * g);
 #pragma unroll
                 for (int t = 0; t < kTW; ++t) {
@@ -190,25 +213,33 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
             }
         }
     };
+    // One K block: the stage two blocks ahead is free once everyone has computed the block before this one; this
+    // wave's chunks of block kb have landed once only the loads issued after them are outstanding (VMEM completes in
+    // order); everyone's have after the barrier.
+    // Barriers are s_barrier with explicit waits: a __syncthreads() fence would wait for every outstanding load,
+    // the next blocks' included (the LDS DMA counts as an LDS write).
+    auto step = [&](int kb, auto st_tag) {
+        constexpr int ST = decltype(st_tag)::value;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // everyone is done with block kb - 1
+        issue(kb + 2, (ST + 2) % kStages, std::integral_constant<int, (ST + 2) % kStages>{});
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(3 * kLoadsPerIssue - kChunks / kWaves) : "memory");
+        sum_spans(ST);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        compute(ST, std::integral_constant<int, ST>{});
+    };
 
-    // prologue: block 0 into LDS buffer 0, block 1's loads in flight
-    issue(0, std::integral_constant<int, 0>{});
-    stage(0);
-    issue(1, std::integral_constant<int, 1>{});
-    __syncthreads();
-    // two K blocks a trip, so that the register slots are constants; block kb computes from LDS buffer kb & 1
-    for (int kb = 0; kb < nkb; kb += 2) {
-        compute(0, std::integral_constant<int, 0>{});
-        if (kb + 1 >= nkb) break;  // uniform
-        stage(1);                  // block kb + 1 (its loads are in xr)
-        issue(kb + 2, std::integral_constant<int, 0>{});
-        __syncthreads();
-        compute(1, std::integral_constant<int, 1>{});
+    issue(0, 0, std::integral_constant<int, 0>{});
+    issue(1, 1, std::integral_constant<int, 1>{});
+    // unrolled by the stage count so that stages and slots are constants (a full unroll hoists every load and
+    // spills)
+    for (int kb = 0; kb < nkb; kb += kStages) {
+        step(kb, std::integral_constant<int, 0>{});
+        if (kb + 1 >= nkb) break;
+        step(kb + 1, std::integral_constant<int, 1>{});
         if (kb + 2 >= nkb) break;
-        stage(0);  // block kb + 2
-        issue(kb + 3, std::integral_constant<int, 1>{});
-        __syncthreads();
+        step(kb + 2, std::integral_constant<int, 2>{});
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the block exits
 
     // ---- stores: D row = token block tb, rows 4g..4g+3; column = the lane's weight row ----
 #pragma unroll
@@ -237,12 +268,7 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
 
 template <int MODE, typename TY>
 hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
-    auto k = gg_kernel<MODE, TY>;
-    const size_t lds = lds_bytes();
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, grid, dim3(kThreads), lds, stream, p);
+    hipLaunchKernelGGL((gg_kernel<MODE, TY>), grid, dim3(kThreads), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -263,14 +289,18 @@ hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int
     const int64_t out_rows = mode == qmm::SWIGLU ? p.N / 2 : p.N;
     const int64_t per_block = mode == qmm::SWIGLU ? kWaves * 16 : kWaves * kTW * 16;
     const dim3 grid((unsigned)wtiles, (unsigned)((out_rows + per_block - 1) / per_block));
+    hipError_t e;
     switch (mode) {
     case qmm::SWIGLU:
-        return out_act == SX_ACT_F32 ? go<qmm::SWIGLU, float>(p, grid, stream) : go<qmm::SWIGLU, uint16_t>(p, grid, stream);
+        e = out_act == SX_ACT_F32 ? go<qmm::SWIGLU, float>(p, grid, stream) : go<qmm::SWIGLU, uint16_t>(p, grid, stream);
+        break;
     case qmm::GATHER:
-        return out_act == SX_ACT_F32 ? go<qmm::GATHER, float>(p, grid, stream) : go<qmm::GATHER, uint16_t>(p, grid, stream);
+        e = out_act == SX_ACT_F32 ? go<qmm::GATHER, float>(p, grid, stream) : go<qmm::GATHER, uint16_t>(p, grid, stream);
+        break;
     default:
-        return go<qmm::COMBINE, float>(p, grid, stream);
+        e = go<qmm::COMBINE, float>(p, grid, stream);
     }
+    return e;
 }
 
 }  // namespace sx::gg
