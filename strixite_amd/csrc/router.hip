@@ -105,6 +105,82 @@ __global__ void __launch_bounds__(256) linear_f32w_kernel(const TX *x, const flo
     project_rows<TX, NT>(x, W, y, M, N, K, part);
 }
 
+// ---------------- router projection at prefill width (M >= 64, BF16 x): MFMA ----------------
+// Each FP32 weight is the exact sum of three BF16 terms (hi = rne(w), mid = rne(w - hi), lo = rne(w - hi - mid)), so
+// x . W = x . hi + x . mid + x . lo with every product exact in v_mfma_f32_16x16x32_bf16 and FP32 accumulation, as
+// the scalar kernel's. A wave owns 16 weight rows x 64 tokens (4 MFMA tiles sharing each split weight fragment); a
+// block 64 rows x 64 tokens. The weight is read once per 64 tokens instead of once per 8.
+typedef __bf16 pw_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float pw_f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kPwTok = 64, kPwRows = 64, kPwMinTokens = 64;
+
+__device__ __forceinline__ void split3(const float4 &a, const float4 &b, pw_bf16x8 &hi, pw_bf16x8 &mid, pw_bf16x8 &lo) {
+    // hardware RNE conversions (v_cvt_pk_bf16_f32); the weights are finite, so NaN payloads never matter here
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const __bf16 h = (__bf16)v[j];
+        const float r1 = v[j] - (float)h;
+        const __bf16 m = (__bf16)r1;
+        hi[j] = h, mid[j] = m, lo[j] = (__bf16)(r1 - (float)m);
+    }
+}
+
+__global__ void __launch_bounds__(256) linear_f32w_mfma_kernel(const uint16_t *x, const float *W, float *y, int64_t M,
+                                                               int64_t N, int64_t K) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n16 = lane & 15, g = lane >> 4;
+    const int64_t row = (int64_t)blockIdx.x * kPwRows + wave * 16 + n16, t0 = (int64_t)blockIdx.y * kPwTok;
+    const float *wr = W + min(row, N - 1) * K + g * 8;
+    const uint16_t *xr[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) xr[tt] = x + min(t0 + tt * 16 + n16, M - 1) * K + g * 8;
+    pw_f32x4 acc[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) acc[tt] = pw_f32x4{0.f, 0.f, 0.f, 0.f};
+    // kPwDepth K steps of loads in flight: step s + kPwDepth is issued into the slot step s frees (K steps past the
+    // end re-load the last step, never used).
+    constexpr int kPwDepth = 4;
+    const int nk = (int)(K / 32);
+    float4 wb[kPwDepth][2];
+    pw_bf16x8 ab[kPwDepth][4];
+    auto issue = [&](int step, int slot) {
+        const int64_t k0 = (int64_t)min(step, nk - 1) * 32;
+        wb[slot][0] = *reinterpret_cast<const float4 *>(wr + k0), wb[slot][1] = *reinterpret_cast<const float4 *>(wr + k0 + 4);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) ab[slot][tt] = *reinterpret_cast<const pw_bf16x8 *>(xr[tt] + k0);
+    };
+#pragma unroll
+    for (int d = 0; d < kPwDepth; ++d) issue(d, d);
+    for (int s0 = 0; s0 < nk; s0 += kPwDepth) {
+#pragma unroll
+        for (int d = 0; d < kPwDepth; ++d) {
+            const float4 wa = wb[d][0], wc = wb[d][1];
+            pw_bf16x8 A[4];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) A[tt] = ab[d][tt];
+            issue(s0 + d + kPwDepth, d);
+            if (s0 + d < nk) {  // uniform
+                pw_bf16x8 hi, mid, lo;
+                split3(wa, wc, hi, mid, lo);
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) {
+                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[tt], lo, acc[tt], 0, 0, 0);
+                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[tt], mid, acc[tt], 0, 0, 0);
+                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[tt], hi, acc[tt], 0, 0, 0);
+                }
+            }
+        }
+    }
+    if (row >= N) return;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t t = t0 + tt * 16 + 4 * g + v;
+            if (t < M) y[t * N + row] = acc[tt][v];
+        }
+}
+
 // ---------------- top-k router: one wave a token (routing::route_token) ----------------
 template <typename T, int NV>
 __global__ void __launch_bounds__(64) moe_router_kernel(const T *logits, int64_t ld, int E, int k, const T *shared,
@@ -158,6 +234,12 @@ int sx_linear_f32w(const void *x, const float *W, int64_t N, int64_t K, float *y
     SX_CHECK((M + kF32wTokens - 1) / kF32wTokens <= 65535, "M = ", M, " too large");
     SX_CHECK((N + kF32wRows - 1) / kF32wRows <= 0x7fffffff, "N = ", N, " too large");
     SX_CHECK(apart(y, M * N * 4, x, M * K * act_bytes(act)) && apart(y, M * N * 4, W, N * K * 4), "y overlaps inputs");
+    if (act == SX_ACT_BF16 && M >= kPwMinTokens && K % 32 == 0 && aligned(x, 16) && (M + kPwTok - 1) / kPwTok <= 65535) {
+        const dim3 g2((unsigned)((N + kPwRows - 1) / kPwRows), (unsigned)((M + kPwTok - 1) / kPwTok));
+        linear_f32w_mfma_kernel<<<g2, 256, 0, stream_of(stream)>>>(static_cast<const uint16_t *>(x), W, y, M, N, K);
+        SX_LAUNCHED("linear_f32w (MFMA) M=", M, " N=", N, " K=", K);
+        return SX_OK;
+    }
     const dim3 grid((unsigned)((N + kF32wRows - 1) / kF32wRows), (unsigned)((M + kF32wTokens - 1) / kF32wTokens));
     if (act == SX_ACT_F32)
         linear_f32w_kernel<float, kF32wTokens><<<grid, 256, 0, stream_of(stream)>>>(static_cast<const float *>(x), W, y,

@@ -136,6 +136,21 @@ def test_router_group_matches_two_calls(M, E, k, act):
     assert np.array_equal(ids.cpu().numpy(), ref_ids)
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 512, 4096), (70, 100, 256), (64, 16, 32)])
+def test_router_projection_prefill_mfma(M, N, K):
+    """Prefill-width router projection (M >= 64, BF16 x: the MFMA path with the FP32 weight as three exact BF16
+    terms) against the oracle's FP64 product, partial token and row tiles included; FP32 accuracy."""
+    import torch
+    rng = np.random.default_rng(M + N)
+    x = util.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    y = kx().linear_f32w(util.bf16_dev(x), torch.from_numpy(W).cuda())
+    sync()
+    ref = orc.linear_f32w(x, W)
+    got = y.cpu().numpy()
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
 # ---------------- experts ----------------
 
 def make_experts(seed, E, I, d, G=128):
