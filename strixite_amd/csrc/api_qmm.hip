@@ -2,14 +2,8 @@
 // Host-side preconditions follow the reference launchers (kernels/linear_q4.hip:353-440, linear_q8.hip:192-223,
 // moe_grouped.hip:476-556); the work runs in qmm_impl.hpp.
 #include "common.hpp"
-#include <algorithm>
-#include <vector>
-#include <cstdio>
-#include <map>
 #include "gemm_grouped.hpp"
 #include "qmm.hpp"
-
-#include <cstdlib>
 
 namespace sx {
 namespace {
@@ -61,95 +55,17 @@ int tiles_per_chunk(int64_t total_tiles) {
     const int64_t waves = (int64_t)device_cus() * 8;
     int64_t tpw = (total_tiles + waves - 1) / waves;
     tpw = tpw < 1 ? 1 : tpw > 16 ? 16 : tpw;
-    if (const char *e = getenv("SX_TPW")) tpw = atoi(e);  // TEMP
     return (int)(tpw * qmm::kWaves);
 }
 
 int launch_qmm(const char *fn, int mode, int bits, int act_x, int act_y, Params &p, int64_t units, int64_t rows_out,
                int64_t grid_y, hipStream_t stream) {
-    if (const char *e = getenv("SX_DBG")) p.dbg = atoi(e);
     const int64_t tiles = (rows_out + qmm::kTile - 1) / qmm::kTile;
     p.tiles_per_chunk = tiles_per_chunk(tiles * units);
     p.nchunks = (int)((tiles + p.tiles_per_chunk - 1) / p.tiles_per_chunk);
     const int64_t gx = units * p.nchunks;
     SX_CHECK(gx >= 1 && gx <= 0x7fffffff && grid_y <= 65535, fn, " grid ", gx, " x ", grid_y, " out of range");
-    static int tr_n = 0;  // TEMP trace
-    const char *te = getenv("SX_TRACE");
-    unsigned long long *tb = nullptr;
-    const size_t nw = (size_t)gx * grid_y * qmm::kWaves;
-    if (te && (tr_n++ % 5) == 4) {
-        hipMalloc(&tb, nw * 128);
-        hipMemset(tb, 0, nw * 128);
-        p.trace = tb;
-    }
     SX_HIP(qmm::launch(mode, bits, act_x, act_y, p, dim3((unsigned)gx, (unsigned)grid_y), stream), fn);
-    if (tb) {
-        hipDeviceSynchronize();
-        std::vector<unsigned long long> h(nw * 16);
-        hipMemcpy(h.data(), tb, nw * 128, hipMemcpyDeviceToHost);
-        hipFree(tb);
-        unsigned long long t0 = ~0ull, tend = 0;
-        double d[5] = {0, 0, 0, 0, 0};
-        int n = 0;
-        std::vector<double> starts, ends;
-        double e5 = 0, e6 = 0, e7 = 0;
-        for (size_t w = 0; w < nw; ++w) {
-            const unsigned long long *r = &h[w * 16];
-            if (!r[0] || !r[4]) continue;
-            if (r[5] && r[6] && r[7]) e7 += (double)(r[7] - r[1]), e5 += (double)(r[5] - r[1]), e6 += (double)(r[6] - r[1]);
-            t0 = std::min(t0, r[0]);
-            tend = std::max(tend, r[4]);
-            for (int i = 1; i < 5; ++i) d[i] += (double)(r[i] - r[i - 1]);
-            ++n;
-        }
-        for (size_t w = 0; w < nw; ++w) {
-            const unsigned long long *r = &h[w * 16];
-            if (!r[0] || !r[4]) continue;
-            starts.push_back((r[0] - t0) * 0.01), ends.push_back((r[4] - t0) * 0.01);
-        }
-        double intra = 0;
-        int nb = 0;
-        for (size_t b = 0; b + 4 <= nw; b += 4) {
-            unsigned long long lo = ~0ull, hi = 0;
-            for (int w = 0; w < 4; ++w)
-                if (h[(b + w) * 16 + 4]) lo = std::min(lo, h[(b + w) * 16 + 4]), hi = std::max(hi, h[(b + w) * 16 + 4]);
-            if (hi) intra += (double)(hi - lo), ++nb;
-        }
-        {  // end time by the number of this kernel's blocks on the block's CU
-            std::map<unsigned long long, int> per_cu;
-            for (size_t b = 0; b < nw; b += 4) if (h[b * 16 + 4]) per_cu[(h[b * 16 + 9] << 32) | ((h[b * 16 + 8] >> 8) & 0xFF)]++;
-            std::map<int, std::pair<double, int>> by;
-            for (size_t b = 0; b < nw; b += 4) {
-                if (!h[b * 16 + 4]) continue;
-                const int c = per_cu[(h[b * 16 + 9] << 32) | ((h[b * 16 + 8] >> 8) & 0xFF)];
-                by[c].first += (h[b * 16 + 4] - t0) * 0.01, by[c].second++;
-            }
-            std::map<int, std::pair<double, int>> byx, byse;
-            for (size_t b = 0; b < nw; b += 4) {
-                if (!h[b * 16 + 4]) continue;
-                const int xcc = (int)(h[b * 16 + 9] & 0xF), se = (int)((h[b * 16 + 8] >> 13) & 0x7);
-                const double e = (h[b * 16 + 4] - t0) * 0.01;
-                byx[xcc].first += e, byx[xcc].second++;
-                byse[xcc * 8 + se].first += e, byse[xcc * 8 + se].second++;
-            }
-            fprintf(stderr, "  by XCC:");
-            for (auto &kv : byx) fprintf(stderr, " x%d %d blk %.1f;", kv.first, kv.second.second, kv.second.first / kv.second.second);
-            fprintf(stderr, "\n  by XCC.SE:");
-            for (auto &kv : byse) fprintf(stderr, " %d.%d:%d/%.1f", kv.first / 8, kv.first % 8, kv.second.second, kv.second.first / kv.second.second);
-            fprintf(stderr, "\n");
-            fprintf(stderr, "  CUs used %zu;", per_cu.size());
-            for (auto &kv : by) fprintf(stderr, " %d blocks/CU: %d blocks, mean end %.2f us;", kv.first, kv.second.second, kv.second.first / kv.second.second);
-            fprintf(stderr, "\n");
-        }
-        fprintf(stderr, "  mean spread of wave end times within a block: %.2f us\n", nb ? intra / nb * 0.01 : 0.0);
-        std::sort(starts.begin(), starts.end());
-        std::sort(ends.begin(), ends.end());
-        auto q = [](std::vector<double> &v, double f) { return v.empty() ? 0.0 : v[(size_t)(f * (v.size() - 1))]; };
-        fprintf(stderr, "  stage detail (from decode end): x issued+pre-prime %.2f, first chunk written %.2f, all written %.2f\n", e7 / nw * 0.01, e5 / nw * 0.01, e6 / nw * 0.01);
-        fprintf(stderr, "TRACE %s waves=%d/%zu span=%.2fus decode=%.2f stage=%.2f first_group=%.2f rest=%.2f | start q50=%.2f q90=%.2f max=%.2f | end q10=%.2f q50=%.2f q90=%.2f max=%.2f\n",
-                fn, n, nw, (tend - t0) * 0.01, d[1] / n * 0.01, d[2] / n * 0.01, d[3] / n * 0.01, d[4] / n * 0.01,
-                q(starts, .5), q(starts, .9), q(starts, 1), q(ends, .1), q(ends, .5), q(ends, .9), q(ends, 1));
-    }
     return SX_OK;
 }
 

@@ -53,8 +53,6 @@ struct Params {
     int nchunks;          // row chunks per unit
     int tiles_per_chunk;  // 16-row tiles (SWIGLU: tile pairs) per chunk
     int max_rows;         // LDS rows staged per unit (tokens in a tile; SLOT_COMBINE: A)
-    int dbg;              // TEMP debug flags
-    unsigned long long *trace;  // TEMP
 };
 
 // Dynamic LDS bytes for a launch: `rows` staged x rows as nsplit BF16 planes; their sums over each run of min(G, span)

@@ -182,10 +182,6 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
     const int unit = (int)(blockIdx.x / (unsigned)p.nchunks), chunk = (int)(blockIdx.x % (unsigned)p.nchunks);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps the loop control scalar
-    unsigned long long *trc = p.trace ? p.trace + ((size_t)(blockIdx.y * gridDim.x + blockIdx.x) * kWaves + wave) * 16 : nullptr;  // TEMP
-#define TRC(i) do { if (trc && lane == 0) trc[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
-    TRC(0);
-    if (trc && lane == 0) trc[8] = __builtin_amdgcn_s_getreg(0xF804), trc[9] = __builtin_amdgcn_s_getreg(0xF814);
 
     // ---- the unit: its activation rows, output rows and expert. Wave 0 decodes it, lane r filling row r, so a
     // unit costs one or two dependent memory latencies rather than one a row. ----
@@ -245,7 +241,6 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
     }
     __syncthreads();
     const int T_all = __builtin_amdgcn_readfirstlane(s_T), R = __builtin_amdgcn_readfirstlane(s_R);
-    TRC(1);
     if (T_all == 0) return;  // an over-provisioned grouped unit: uniform for the block
     const int tiles_total = (int)((Nrows + kTile - 1) / kTile);
     const int tile0 = chunk * p.tiles_per_chunk;
@@ -300,7 +295,7 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
     // arrive as one contiguous window per row (8 or 16 bytes). (q4 K = 4096 / 1024, G = 128 and q8 K = 4096,
     // G = 64 / 128 all qualify.)
     constexpr int SPG = kPrefetch / NW;  // spans a group = quantization groups it covers (G is one span)
-    const bool fast = qlast == 0 && ngs == 1 && gshift == 0 && ngroups % SPG == 0 && nspan % SPG == 0 && !(p.dbg & 1);
+    const bool fast = qlast == 0 && ngs == 1 && gshift == 0 && ngroups % SPG == 0 && nspan % SPG == 0;
     uint4 ring[kRing][kPrefetch];
     uint4 sw_n[kRing][NW], mw_n[kRing][NW];
     int ic = 0, ia = 0, ip = 0, ii = 0;  // issue cursor: span, segment, pass, tile
@@ -430,7 +425,6 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
                 raw[b] = load_raw8(x + s_xrow[i >> lg_chunks] + (int64_t)(i & (chunks8 - 1)) * 8);
             }
             __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
-            TRC(7);
             prime();  // unconditional (a wave without tiles reads a clamped, valid row): a branch here would make the
                       // activation waits below count the weight loads too
             __builtin_amdgcn_sched_barrier(0);
@@ -452,7 +446,6 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
                         else xsum[(size_t)rn * 16 + r] = sum;
                     }
                 }
-                if (b == 0) TRC(5);
             }
         };
         const int nb = (n_items + kThreads - 1) / kThreads;  // uniform
@@ -460,9 +453,7 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
         else if (nb <= 4) stage_and_prime(std::integral_constant<int, 4>{});
         else if (kStageMax > 4 && nb <= 8) stage_and_prime(std::integral_constant<int, (kStageMax > 4 ? 8 : 4)>{});
         else stage_and_prime(std::integral_constant<int, kStageMax>{});
-        TRC(6);
         __syncthreads();
-        TRC(2);
         if (my_tiles <= 0) return;
         int cc = 0, ca = 0, cp = 0, ci = 0;  // consume cursor
         f32x4 acc[NW];
@@ -547,12 +538,10 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
         // The ring slot of group gr is gr % kRing: the loop takes kRing groups a trip so that slots are constants.
         for (int gr = 0; gr < groups; gr += kRing) {
             consume(gr, std::integral_constant<int, 0>{});
-            if (gr == 0) TRC(3);
             if (gr + 1 < groups) consume(gr + 1, std::integral_constant<int, 1>{});
             if constexpr (kRing > 2) if (gr + 2 < groups) consume(gr + 2, std::integral_constant<int, (kRing > 2 ? 2 : 0)>{});
             if constexpr (kRing > 3) if (gr + 3 < groups) consume(gr + 3, std::integral_constant<int, (kRing > 3 ? 3 : 0)>{});
         }
-        TRC(4);
         return;
     }
 
@@ -565,7 +554,6 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
 
     stage(b0, Rb);
     __syncthreads();
-    TRC(2);
     npass = (T + TP - 1) / TP;
     if (my_tiles > 0) {
     const int per_tile = npass * nseg * nspan * NW;
