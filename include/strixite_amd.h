@@ -92,6 +92,24 @@ int sx_moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, voi
 int sx_moe_router_group(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int act, int32_t *ids,
                         float *coef, uint32_t *router_err, void *ws, size_t ws_bytes, uint32_t *expert_err,
                         sx_stream stream);
+/* ---- verify-width MoE FFN in two launches (after the router projection) ----
+ * The sequence runtime/qwen4exp.cpp:1139-1163 runs below kGroupedMinTokens - moe_router (moe_router.hpp:38-40),
+ * linear_q4_experts_gather_swiglu (linear_q4.hpp:55-56), linear_q4_experts_combine (linear_q4.hpp:44-46) - with the
+ * same ids, coef, h, y and error words; no reference counterpart as two calls. q4 G = 128, BF16 activations;
+ * M <= 16, M * A <= 64 (A = k + 1 with a shared slot), gate_up K in {512 .. 4096}, down K in {1024, 2048};
+ * sx_moe_verify_supported says whether a shape qualifies (SX_OK) or why not. Ew: experts stacked in the weights
+ * (E, or E + 1 with the shared expert stacked). A repeated id within a token counts as an invalid slot. */
+int sx_moe_verify_supported(int64_t M, int64_t A, int64_t E, int64_t k, int64_t Ew, const sx_qview *gate_up,
+                            const sx_qview *down, int act);
+/* route (ids, coef [M, A]; router_err) + h [M, A, I] = silu(x W_gate^T) * (x W_up^T) per slot (expert_err, NaN rows
+ * for invalid slots). shared_logit nullable. */
+int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
+                          const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *gate_up,
+                          int64_t Ew, int32_t *ids, float *coef, void *h, int act, uint32_t *router_err,
+                          uint32_t *expert_err, sx_stream stream);
+/* y [M, N] = sum_a coef[m, a] * (h[m, a] W_down[ids[m, a]]^T); NaN rows for tokens with an invalid slot. */
+int sx_moe_verify_down(const void *h, int64_t M, int64_t A, const int32_t *ids, const float *coef,
+                       const sx_qview *down, int64_t Ew, void *y, int act, uint32_t *expert_err, sx_stream stream);
 /* y [M, A, N] (linear_q4_experts_gather_grouped, moe_grouped.hpp:53-55). */
 int sx_linear_q4_experts_gather_grouped(const void *x, const sx_qview *w, int64_t E, const void *ws, size_t ws_bytes,
                                         int64_t M, int64_t A, void *y, int act, int math, sx_stream stream);

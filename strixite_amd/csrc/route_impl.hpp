@@ -22,29 +22,45 @@ __device__ __forceinline__ float key_value(uint64_t key) {
     return __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
 }
 
-// Wave-wide maximum of 64-bit keys, all in DPP (no LDS round trips): inside each row of 16 lanes quad [1,0,3,2],
-// quad [2,3,0,1], half-row mirror and row mirror leave every lane with its row's maximum (max needs no particular
-// pairing); then row_bcast:15 (rows 1, 3 take lane 15 of the row before) and row_bcast:31 (rows 2, 3 take lane 31)
-// leave the wave's maximum in lane 63, read out as a scalar.
+// Wave-wide reductions of one 32-bit value, all in DPP (no LDS round trips): inside each row of 16 lanes quad
+// [1,0,3,2], quad [2,3,0,1], half-row mirror and row mirror leave every lane with its row's result (max, min and
+// sum need no particular pairing); then row_bcast:15 (rows 1, 3 take lane 15 of the row before) and row_bcast:31
+// (rows 2, 3 take lane 31) leave the wave's result in lane 63, read out as a scalar. A row outside a broadcast's row
+// mask receives `old`: the value itself for max / min, 0 for sum.
 template <int CTRL, int ROWS = 0xF>
-__device__ __forceinline__ uint64_t dpp_max(uint64_t k) {
-    const int lo0 = (int)(uint32_t)k, hi0 = (int)(uint32_t)(k >> 32);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(lo0, lo0, CTRL, ROWS, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(hi0, hi0, CTRL, ROWS, 0xF, false);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    return o > k ? o : k;
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xF, false);
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-    k = dpp_max<0xB1>(k);        // quad_perm [1,0,3,2]
-    k = dpp_max<0x4E>(k);        // quad_perm [2,3,0,1]
-    k = dpp_max<0x141>(k);       // row_half_mirror
-    k = dpp_max<0x140>(k);       // row_mirror
-    k = dpp_max<0x142, 0xA>(k);  // row_bcast:15 into rows 1 and 3
-    k = dpp_max<0x143, 0xC>(k);  // row_bcast:31 into rows 2 and 3
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 63);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v, v));
+    v = max(v, dpp_u32<0x4E>(v, v));
+    v = max(v, dpp_u32<0x141>(v, v));
+    v = max(v, dpp_u32<0x140>(v, v));
+    v = max(v, dpp_u32<0x142, 0xA>(v, v));
+    v = max(v, dpp_u32<0x143, 0xC>(v, v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0xB1>(v, v));
+    v = min(v, dpp_u32<0x4E>(v, v));
+    v = min(v, dpp_u32<0x141>(v, v));
+    v = min(v, dpp_u32<0x140>(v, v));
+    v = min(v, dpp_u32<0x142, 0xA>(v, v));
+    v = min(v, dpp_u32<0x143, 0xC>(v, v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ float wave_sum_f32(float x) {
+    auto add = [](float a, uint32_t b) { return a + __uint_as_float(b); };
+    x = add(x, dpp_u32<0xB1>(0u, __float_as_uint(x)));
+    x = add(x, dpp_u32<0x4E>(0u, __float_as_uint(x)));
+    x = add(x, dpp_u32<0x141>(0u, __float_as_uint(x)));
+    x = add(x, dpp_u32<0x140>(0u, __float_as_uint(x)));
+    x = add(x, dpp_u32<0x142, 0xA>(0u, __float_as_uint(x)));
+    x = add(x, dpp_u32<0x143, 0xC>(0u, __float_as_uint(x)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
 
 // Sorts N (a power of two) keys descending in registers: a bitonic network with compile-time indices.
@@ -66,29 +82,33 @@ __device__ __forceinline__ void sort_desc(uint64_t (&a)[N]) {
             }
 }
 
-// Token m's routing by one wave: the E logits (load(e) -> float) stay in registers, lane l holding experts
-// l, l + 64, ...; k rounds of a wave-wide key maximum, only the lane whose expert was picked rescanning its
-// registers; then the softmax over the k picks (coef = exp(l - l_max) / sum). A non-finite logit (or shared gate)
-// fails the token: ids -1, coefficients NaN, err = {1, m, expert} (first wins). With has_shared, slot k is the
-// shared expert with coefficient sigmoid(sl). lds_row (may be null) receives the ids too.
+// Lane l's NV logits of one token (experts l, l + 64, ...; past E: expert E - 1 again, masked later). Every lane
+// loads all NV, so the loads go out together and one wait covers them (a load under a per-lane condition becomes a
+// branch with its own wait).
 template <int NV, typename Load>
-__device__ void route_token(Load load, int E, int k, bool has_shared, float sl, int32_t shared_id, int64_t m,
-                            int32_t *id_row, float *coef_row, int32_t *lds_row, uint32_t *err) {
+__device__ __forceinline__ void load_logits(Load load, int E, float (&v)[NV]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) v[j] = load(min(lane + 64 * j, E - 1));
+}
+
+// route_token on logits already in registers (load_logits).
+template <int NV>
+__device__ void route_values(float (&v)[NV], int E, int k, bool has_shared, float sl, int32_t shared_id, int64_t m,
+                             int32_t *id_row, float *coef_row, int32_t *lds_row, uint32_t *err) {
     const int lane = threadIdx.x & 63;
     const int A = k + (has_shared ? 1 : 0);
-    float v[NV];
     int bad = INT_MAX;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int e = lane + 64 * j;
-        const float xv = e < E ? load(e) : -INFINITY;
-        v[j] = xv;
-        if (e < E && !isfinite(xv) && e < bad) bad = e;
+        v[j] = e < E ? v[j] : -INFINITY;
+        if (e < E && !isfinite(v[j]) && e < bad) bad = e;
     }
     if (has_shared && !isfinite(sl) && E < bad) bad = E;
-    for (int off = 32; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off));
+    if (__ballot(bad != INT_MAX)) bad = (int)wave_min_u32((uint32_t)bad);  // uniform; INT_MAX: no bad logit
     if (bad != INT_MAX) {  // kernels/moe_router.hpp:19-23
-        if (lane == 0) flag_error(err, (uint32_t)m, (uint32_t)bad);
+        if (lane == 0 && err) flag_error(err, (uint32_t)m, (uint32_t)bad);  // null err: a redundant copy of the routing
         for (int a = lane; a < A; a += 64) {
             id_row[a] = -1, coef_row[a] = qnan();
             if (lds_row) lds_row[a] = -1;
@@ -104,22 +124,30 @@ __device__ void route_token(Load load, int E, int k, bool has_shared, float sl, 
         keys[j] = e < E ? route_key(v[j], e) : 0;
     }
     sort_desc<NV>(keys);
+    // A round: the wave maximum of the lane heads' value keys (32-bit DPP); a tie between lanes goes to the lower
+    // expert index (a second reduction, only then); the lane that owned the winner pops its head.
+    uint32_t hv[NV], hx[NV];  // value key (the monotone bits), expert index; padding: 0, 0xFFFFFFFF
+#pragma unroll
+    for (int j = 0; j < NV; ++j) hv[j] = (uint32_t)(keys[j] >> 32), hx[j] = 0xFFFFFFFFu - (uint32_t)keys[j];
     float my_v = -INFINITY, top = 0.f;
     int my_i = -1;
     for (int r = 0; r < k; ++r) {
-        const uint64_t best = wave_max_u64(keys[0]);  // uniform
-        const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
-        const float bv = key_value(best);
+        const uint32_t best = wave_max_u32(hv[0]);  // uniform
+        const bool cand = hv[0] == best;
+        const uint64_t cands = __ballot(cand);
+        const uint32_t bi = __popcll(cands) == 1 ? (uint32_t)__builtin_amdgcn_readlane((int)hx[0], __builtin_ctzll(cands))
+                                                 : wave_min_u32(cand ? hx[0] : 0xFFFFFFFFu);
+        const float bv = key_value((uint64_t)best << 32);
         if (r == 0) top = bv;
-        if (lane == r) my_v = bv, my_i = bi;
-        const bool pop = keys[0] == best;  // one lane: keys are distinct
+        if (lane == r) my_v = bv, my_i = (int)bi;
+        const bool pop = cand && hx[0] == bi;  // one lane: a lane's indices are distinct
 #pragma unroll
-        for (int j = 0; j + 1 < NV; ++j) keys[j] = pop ? keys[j + 1] : keys[j];
-        keys[NV - 1] = pop ? 0 : keys[NV - 1];
+        for (int j = 0; j + 1 < NV; ++j) hv[j] = pop ? hv[j + 1] : hv[j], hx[j] = pop ? hx[j + 1] : hx[j];
+        hv[NV - 1] = pop ? 0u : hv[NV - 1];
+        hx[NV - 1] = pop ? 0xFFFFFFFFu : hx[NV - 1];
     }
     const float ex = lane < k ? expf(my_v - top) : 0.f;
-    float sum = ex;
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float sum = wave_sum_f32(ex);
     if (lane < k) {
         id_row[lane] = my_i, coef_row[lane] = ex / sum;
         if (lds_row) lds_row[lane] = my_i;
@@ -128,6 +156,19 @@ __device__ void route_token(Load load, int E, int k, bool has_shared, float sl, 
         id_row[k] = shared_id, coef_row[k] = 1.0f / (1.0f + expf(-sl));
         if (lds_row) lds_row[k] = shared_id;
     }
+}
+
+// Token m's routing by one wave: the E logits (load(e) -> float) stay in registers, lane l holding experts
+// l, l + 64, ...; k rounds of a wave-wide key maximum, only the lane whose expert was picked rescanning its
+// registers; then the softmax over the k picks (coef = exp(l - l_max) / sum). A non-finite logit (or shared gate)
+// fails the token: ids -1, coefficients NaN, err = {1, m, expert} (first wins). With has_shared, slot k is the
+// shared expert with coefficient sigmoid(sl). lds_row (may be null) receives the ids too.
+template <int NV, typename Load>
+__device__ void route_token(Load load, int E, int k, bool has_shared, float sl, int32_t shared_id, int64_t m,
+                            int32_t *id_row, float *coef_row, int32_t *lds_row, uint32_t *err) {
+    float v[NV];
+    load_logits<NV>(load, E, v);
+    route_values<NV>(v, E, k, has_shared, sl, shared_id, m, id_row, coef_row, lds_row, err);
 }
 
 // Exclusive prefix sums of three per-thread counts over an NT-thread block: wave64 inclusive scans by shuffles,

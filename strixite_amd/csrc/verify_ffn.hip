@@ -1,0 +1,593 @@
+// Verify-width MoE FFN in two launches after the router projection: the sequence runtime/qwen4exp.cpp:1139-1163
+// runs below kGroupedMinTokens (moe_router, linear_q4_experts_gather_swiglu, linear_q4_experts_combine) with the
+// same outputs, re-laid for one MI355X:
+//
+//   gate_up_kernel: every block routes all M tokens itself from the logits (routing::route_token, a wave a token;
+//     M * k <= 64 slots, so this is a few microseconds and saves a launch plus the dependent workspace reads of a
+//     separate grouping step), lists the distinct experts in id order with their token masks, stages all M
+//     activation rows in LDS once, and takes an equal share of the (expert, 16-feature tile) items - equal per
+//     wave to within one item, so every CU streams the same number of weight bytes. An item is one MFMA pass of
+//     gate and up over all M tokens (the rows of a 16x16 MFMA tile cost the same filled or not); the epilogue
+//     stores SwiGLU(gate, up) to the slots of the tokens routed to the expert. Block 0 also writes ids, coef and
+//     the error words.
+//   down_kernel: a block owns 16 output rows for all tokens, its 8 waves split the distinct experts, each expert's
+//     tile is read once for all its tokens, and y[m] = sum_e coef[m, e] * (h[slot(m, e)] . W[e]) is summed per
+//     wave in expert order, then across the waves in LDS in a fixed order: deterministic, no FP32 partials in
+//     memory and no separate combine.
+//
+// Both stream their weight tiles with the scheme of qmm_impl.hpp's fast path: a lane loads 16 code bytes a step
+// (16 rows x one 64-byte span a wave), groups of 8 steps with their scale / min windows, 2 groups in flight, and
+// v_mfma_f32_16x16x32_bf16 on BF16 (128 + code) against the LDS-staged activations:
+//   sum_k x * (code * s + m) = s * D + (m - 128 s) * sum_span x.
+#include "qmm_impl.hpp"
+#include "route_impl.hpp"
+#include "verify_ffn.hpp"
+
+namespace sx::vf {
+namespace {
+
+using qmm::detail::bf16x8;
+using qmm::detail::f32x4;
+using qmm::detail::kPrefetch;
+
+constexpr int kThreads = 512, kWaves = 8;
+constexpr int kRing = 2;  // groups of 8 loads in flight a wave (16 KB a wave, 128 KB a CU; 3 measured slower)
+constexpr int kSpan = 128, kSpanBytes = 64;
+constexpr int kZeroBytes = qmm::detail::kZeroBytes;
+
+struct Routes {                // one block's copy of the routing (LDS)
+    int32_t ids[kMaxSlots];    // slot s = m * A + a
+    float coef[kMaxSlots];
+    int32_t u_exp[kMaxSlots];  // distinct valid experts, ascending
+    uint32_t u_mask[kMaxSlots];  // their tokens (bit m)
+    int U;
+    uint64_t bad_slots;        // invalid slots: id outside [0, Ew) or repeated within its token
+    int wtot[kWaves][3];
+    int8_t slot_tab[kMaxSlots][kMaxTokens];  // [unit][token]: the token's slot of the unit's expert, or -1
+};
+
+// The distinct experts of the slots in id order with their token masks. bad_slots marks ids outside [0, Ew) and
+// repeats of an id within a token (the routers never produce one; such a slot is treated as invalid).
+// emask: LDS [Ew]. Expects R.ids written and a barrier since; ends with a barrier.
+__device__ void build_units(Routes &R, uint32_t *emask, int S, int A, int Ew) {
+    const int t = threadIdx.x;
+    for (int e = t; e < Ew; e += kThreads) emask[e] = 0;
+    if (t < 64) {
+        bool bad = false;
+        if (t < S) {
+            const int32_t id = R.ids[t];
+            bad = !(id >= 0 && id < Ew);
+            for (int s = t - t % A; s < t; ++s) bad |= R.ids[s] == id;
+        }
+        const uint64_t mask = __ballot(bad);
+        if (t == 0) R.bad_slots = mask;
+    }
+    __syncthreads();
+    if (t < S && !((R.bad_slots >> t) & 1ull)) atomicOr(&emask[R.ids[t]], 1u << (t / A));
+    __syncthreads();
+    const int per = (Ew + kThreads - 1) / kThreads;
+    const int b0 = min(t * per, Ew), b1 = min(b0 + per, Ew);
+    int v[3] = {0, 0, 0}, ex[3], tot[3];
+    for (int b = b0; b < b1; ++b) v[0] += emask[b] != 0;
+    routing::block_scan3<kThreads>(v, ex, tot, R.wtot);
+    int pos = ex[0];
+    for (int b = b0; b < b1; ++b) {  // emask[b] becomes the unit index of expert b (read only for valid slots)
+        const uint32_t mk = emask[b];
+        if (mk) R.u_exp[pos] = b, R.u_mask[pos] = mk, emask[b] = pos++;
+    }
+    if (t == 0) R.U = tot[0];
+    for (int i = t; i < kMaxSlots * kMaxTokens; i += kThreads) (&R.slot_tab[0][0])[i] = -1;
+    __syncthreads();
+    if (t < S && !((R.bad_slots >> t) & 1ull)) R.slot_tab[emask[R.ids[t]]][t / A] = (int8_t)t;
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// gate_up + SwiGLU. LDS (static): the M activation rows [M][K + 8] BF16 in the B operand's code order, their span
+// sums [K / 128][16] and a zero block for the MFMA rows past M.
+template <int NV, int NB>
+__global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[kXsElems];
+    __shared__ __attribute__((aligned(16))) float xsum[kMaxSpansGu * 16];
+    __shared__ __attribute__((aligned(16))) uint16_t zero_block[kZeroBytes / 2];
+    __shared__ Routes R;
+    __shared__ uint32_t emask[kMaxExperts];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = p.M, A = p.A, S = M * A, Ew = p.Ew;
+    const int64_t K = p.K, ldx = K + 8;
+    const int nspan = (int)(K / kSpan), chunks8 = (int)(K / 8), lg_chunks = __builtin_ctz((unsigned)chunks8);
+    const int n_items_x = M * chunks8;
+
+    // 1. this wave's logits (tokens wave and wave + 8, clamped: a redundant row past M), then the activations: the
+    // routing waits for its own loads only
+    const float *row0 = p.logits + (int64_t)min(wave, M - 1) * p.ld, *row1 = p.logits + (int64_t)min(wave + kWaves, M - 1) * p.ld;
+    float v0[NV], v1[NV];
+    routing::load_logits<NV>([&](int e) { return row0[e]; }, p.E, v0);
+    routing::load_logits<NV>([&](int e) { return row1[e]; }, p.E, v1);
+    const float sl0 = p.shared_logit ? p.shared_logit[(int64_t)min(wave, M - 1) * p.shared_ld] : 0.f;
+    const float sl1 = p.shared_logit ? p.shared_logit[(int64_t)min(wave + kWaves, M - 1) * p.shared_ld] : 0.f;
+    uint4 raw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int i = min(b * kThreads + tid, n_items_x - 1);
+        raw[b] = *reinterpret_cast<const uint4 *>(p.x + (int64_t)(i >> lg_chunks) * K + (int64_t)(i & (chunks8 - 1)) * 8);
+    }
+    for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(zero_block)[i] = 0u;
+
+    // 2. routing, a wave a token (moe_router.hpp:11-23); only block 0 reports errors and writes ids / coef out
+    const bool lead = blockIdx.x == 0;
+    if (wave < M)
+        routing::route_values<NV>(v0, p.E, p.k, p.shared_logit != nullptr, sl0, p.shared_id, wave, R.ids + wave * A,
+                                  R.coef + wave * A, nullptr, lead ? p.router_err : nullptr);
+    if (wave + kWaves < M)
+        routing::route_values<NV>(v1, p.E, p.k, p.shared_logit != nullptr, sl1, p.shared_id, wave + kWaves,
+                                  R.ids + (wave + kWaves) * A, R.coef + (wave + kWaves) * A, nullptr,
+                                  lead ? p.router_err : nullptr);
+    __syncthreads();
+    build_units(R, emask, S, A, Ew);
+    const int U = __builtin_amdgcn_readfirstlane(R.U);
+    const int64_t Nrows = p.N / 2, rowbytes = K / 2, ngroups = K / kSpan;
+    if (lead) {
+        if (tid < S) p.ids[tid] = R.ids[tid], p.coef[tid] = R.coef[tid];
+        uint64_t bad = R.bad_slots;  // invalid slots: error words (first slot wins) and NaN rows
+        if (bad && tid == 0) {
+            const int s = __builtin_ctzll(bad);
+            flag_error(p.expert_err, (uint32_t)R.ids[s], (uint32_t)s);
+        }
+        while (bad) {
+            const int s = __builtin_ctzll(bad);
+            bad &= bad - 1;
+            for (int64_t n = tid; n < Nrows; n += kThreads) p.h[s * Nrows + n] = (uint16_t)f32_to_bf16(qnan());
+        }
+    }
+
+    // 3. this wave's items: [i0, i1) of U x T16 (expert-major), split evenly over every wave of the grid
+    const int T16 = (int)((Nrows + 15) / 16);
+    const int64_t F = (int64_t)U * T16, W = (int64_t)gridDim.x * kWaves, gw = (int64_t)blockIdx.x * kWaves + wave;
+    const int i0 = (int)(gw * F / W), my = (int)((gw + 1) * F / W) - i0;
+
+    // 4. weight ring: gate and up alternate, SPG = 4 spans (groups) a ring group, scale / min windows of 4 BF16
+    constexpr int NW = 2, SPG = kPrefetch / NW;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int64_t up_q = Nrows * rowbytes, up_g = Nrows * ngroups;
+    const int groups = my * (nspan / SPG);
+    uint4 ring[kRing][kPrefetch];
+    uint2 sw_n[kRing][NW], mw_n[kRing][NW];
+    int ic = 0, ii = 0;
+    const uint8_t *iq = p.q;
+    const uint16_t *is_ = p.scale, *im = p.minv;
+    auto iplace = [&]() {  // item i0 + ii (clamped into the item range; F > 0 here)
+        const int item = (int)min((int64_t)(i0 + ii), F - 1);
+        const int u = item / T16, tile = item - u * T16;
+        const int64_t n = (int64_t)tile * 16 + n16, nn = n < Nrows ? n : Nrows - 1;
+        const int64_t row = (int64_t)R.u_exp[u] * p.N + nn;
+        iq = p.q + row * rowbytes + g * 16;
+        is_ = p.scale + row * ngroups;
+        im = p.minv + row * ngroups;
+    };
+    auto advance_issue = [&]() {
+        if (ic + SPG < nspan) {
+            ic += SPG;
+            return;
+        }
+        ic = 0, ++ii;
+        iplace();
+    };
+    auto issue_window = [&](uint2 (&sw)[NW], uint2 (&mw)[NW]) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            sw[w] = *reinterpret_cast<const uint2 *>(is_ + (w ? up_g : 0) + ic);
+            mw[w] = *reinterpret_cast<const uint2 *>(im + (w ? up_g : 0) + ic);
+        }
+    };
+    auto issue_slot = [&](uint4 (&slot)[kPrefetch], int s) {
+        const int span = ic + s / NW, w = s % NW;
+        slot[s] = *reinterpret_cast<const uint4 *>(iq + (w ? up_q : 0) + (int64_t)span * kSpanBytes);
+    };
+    if (U == 0) return;  // uniform: every slot invalid (handled above)
+    __builtin_amdgcn_sched_barrier(0);
+    iplace();
+#pragma unroll
+    for (int r = 0; r < kRing; ++r) {
+        if (r > 0 && r < groups) advance_issue();
+        issue_window(sw_n[r], mw_n[r]);
+#pragma unroll
+        for (int s = 0; s < kPrefetch; ++s) issue_slot(ring[r], s);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 5. activations into LDS (q4 code order) with their span sums
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int i = b * kThreads + tid;
+        if (i < n_items_x) {  // a span's 16 lanes are all in or all out (kThreads, chunks8 are multiples of 16)
+            const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
+            uint4 planes[1];
+            float sum;
+            qmm::detail::chunk_planes<4, 1, uint16_t>(raw[b], planes, sum);
+            *reinterpret_cast<uint4 *>(xs + r * ldx + (int64_t)c8 * 8) = planes[0];
+            sum = qmm::detail::group_sum_c<16>(sum);
+            if ((c8 & 15) == 0) xsum[(c8 >> 4) * 16 + r] = sum;
+        }
+    }
+    for (int i = tid; i < nspan * 16; i += kThreads)
+        if ((i & 15) >= M) xsum[i] = 0.f;
+    __syncthreads();
+    if (my <= 0) return;
+
+    // 6. consume: A rows = tokens (lane row n16), D rows 4g .. 4g + 3 = tokens, columns = the 16 features
+    const bool a_on = n16 < M;
+    const uint16_t *a_row = a_on ? xs + n16 * ldx + g * 32 : zero_block;
+    const int64_t a_step = a_on ? kSpan : 0;  // the zero block is re-read for every span
+    int cc = 0, ci = 0;
+    f32x4 acc[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](int gr, auto slot_tag) {
+        constexpr int RS = decltype(slot_tag)::value;
+        uint2 sw[NW], mw[NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sw[w] = sw_n[RS][w], mw[w] = mw_n[RS][w];
+        if (gr + kRing < groups) advance_issue();
+        issue_window(sw_n[RS], mw_n[RS]);
+        const uint16_t *ab = a_row + cc * a_step;
+        const float *xsg = xsum + cc * 16 + 4 * g;
+#pragma unroll
+        for (int s = 0; s < kPrefetch; ++s) {
+            const int w = s % NW, so = s / NW;
+            const uint4 w_cur = ring[RS][s];
+            issue_slot(ring[RS], s);
+            f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8 *>(ab + so * a_step + t * 8);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, qmm::detail::codes_b<4>(w_cur, t), D, 0, 0, 0);
+            }
+            const float4 xv = *reinterpret_cast<const float4 *>(xsg + so * 16);
+            const uint32_t swd = so < 2 ? sw[w].x : sw[w].y, mwd = so < 2 ? mw[w].x : mw[w].y;
+            const float s_ = __uint_as_float((so & 1) ? (swd & 0xFFFF0000u) : (swd << 16));
+            const float m_ = __uint_as_float((so & 1) ? (mwd & 0xFFFF0000u) : (mwd << 16));
+            const float cm = fmaf(-128.f, s_, m_);
+            acc[w][0] = fmaf(s_, D[0], fmaf(cm, xv.x, acc[w][0]));
+            acc[w][1] = fmaf(s_, D[1], fmaf(cm, xv.y, acc[w][1]));
+            acc[w][2] = fmaf(s_, D[2], fmaf(cm, xv.z, acc[w][2]));
+            acc[w][3] = fmaf(s_, D[3], fmaf(cm, xv.w, acc[w][3]));
+        }
+        if (gr >= groups) return;  // the phantom group
+        if (cc + SPG < nspan) {
+            cc += SPG;
+            return;
+        }
+        cc = 0;
+        const int item = i0 + ci;
+        const int u = item / T16, tile = item - u * T16;
+        const uint32_t mask = R.u_mask[u];
+        const int64_t n = (int64_t)tile * 16 + n16;
+        if (n < Nrows) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = 4 * g + v;
+                if (r >= M || !((mask >> r) & 1u)) continue;
+                const float gv = as_bf16(acc[0][v]), uv = as_bf16(acc[1][v]);
+                const float hv = as_bf16(silu(gv)) * uv;
+                p.h[(int64_t)R.slot_tab[u][r] * Nrows + n] = (uint16_t)f32_to_bf16(hv);
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+        ++ci;
+    };
+    // Runs of kRing groups, all issuing their loads (a count short of a multiple of kRing ends with phantom groups
+    // that re-load the last one and stop after their MFMAs): a consume whose loads were conditional would merge two
+    // versions of the ring registers, and the copies at such a merge wait for every outstanding load.
+    for (int gr = 0; gr < groups; gr += kRing) {
+        consume(gr, std::integral_constant<int, 0>{});
+        consume(gr + 1, std::integral_constant<int, 1>{});
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// down + combine. LDS (static): the S slot rows of h [S][K + 8] BF16 (code order), span sums [S][K / 128], a zero
+// block, the waves' partial sums [8][16 tokens][16 rows].
+template <int NB>
+__global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t hs[kHsElems];
+    __shared__ __attribute__((aligned(16))) float hsum[kMaxSlots * kMaxSpansDn];
+    __shared__ __attribute__((aligned(16))) uint16_t zero_block[kZeroBytes / 2];
+    __shared__ __attribute__((aligned(16))) float red[kWaves][16][16];
+    __shared__ Routes R;
+    __shared__ uint32_t emask[kMaxExperts];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = p.M, A = p.A, S = M * A, Ew = p.Ew;
+    const int64_t K = p.K, ldh = K + 8, N = p.N;
+    const int nspan = (int)(K / kSpan), chunks8 = (int)(K / 8), lg_chunks = __builtin_ctz((unsigned)chunks8);
+    const int n_items_x = S * chunks8;
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
+
+    // the routing first, then the rows of h: the grouping waits for the ids only
+    int32_t my_id;
+    float my_coef;
+    my_id = p.ids[min(lane, S - 1)], my_coef = p.coef[min(lane, S - 1)];  // every wave: no branch around loads
+    uint4 raw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int i = min(b * kThreads + tid, n_items_x - 1);
+        raw[b] = *reinterpret_cast<const uint4 *>(p.h + (int64_t)(i >> lg_chunks) * K + (int64_t)(i & (chunks8 - 1)) * 8);
+    }
+    R.ids[lane] = my_id, R.coef[lane] = my_coef;  // every wave the same values (unconditional: nothing sinks the loads)
+    for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(zero_block)[i] = 0u;
+    __syncthreads();
+    build_units(R, emask, S, A, Ew);
+    const int U = __builtin_amdgcn_readfirstlane(R.U);
+    const uint64_t bad_slots = R.bad_slots;
+    if (blockIdx.x == 0 && bad_slots && tid == 0) {
+        const int s = __builtin_ctzll(bad_slots);
+        flag_error(p.expert_err, (uint32_t)R.ids[s], (uint32_t)s);
+    }
+
+    const int64_t rowbytes = K / 2, ngroups = K / kSpan;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int my = U > wave ? (U - wave + kWaves - 1) / kWaves : 0;  // units wave, wave + 8, ...
+    constexpr int SPG = kPrefetch;
+    const int groups = my * (nspan / SPG);
+    uint4 ring[kRing][kPrefetch];
+    uint4 sw_n[kRing], mw_n[kRing];
+    int ic = 0, ii = 0;
+    const uint8_t *iq = p.q;
+    const uint16_t *is_ = p.scale, *im = p.minv;
+    auto iplace = [&]() {
+        const int u = min(wave + ii * kWaves, U - 1);  // past the units (or none): a valid row, never used
+        const int64_t n = n0 + n16, nn = n < N ? n : N - 1;
+        const int64_t row = (int64_t)(u >= 0 ? R.u_exp[u] : 0) * N + nn;
+        iq = p.q + row * rowbytes + g * 16;
+        is_ = p.scale + row * ngroups;
+        im = p.minv + row * ngroups;
+    };
+    auto advance_issue = [&]() {
+        if (ic + SPG < nspan) {
+            ic += SPG;
+            return;
+        }
+        ic = 0, ++ii;
+        iplace();
+    };
+    auto issue_window = [&](uint4 &sw, uint4 &mw) {
+        sw = *reinterpret_cast<const uint4 *>(is_ + ic);
+        mw = *reinterpret_cast<const uint4 *>(im + ic);
+    };
+    auto issue_slot = [&](uint4 (&slot)[kPrefetch], int s) {
+        slot[s] = *reinterpret_cast<const uint4 *>(iq + (int64_t)(ic + s) * kSpanBytes);
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    iplace();
+#pragma unroll
+    for (int r = 0; r < kRing; ++r) {
+        if (r > 0 && r < groups) advance_issue();
+        issue_window(sw_n[r], mw_n[r]);
+#pragma unroll
+        for (int s = 0; s < kPrefetch; ++s) issue_slot(ring[r], s);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int i = b * kThreads + tid;
+        if (i < n_items_x) {
+            const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
+            uint4 planes[1];
+            float sum;
+            qmm::detail::chunk_planes<4, 1, uint16_t>(raw[b], planes, sum);
+            *reinterpret_cast<uint4 *>(hs + r * ldh + (int64_t)c8 * 8) = planes[0];
+            sum = qmm::detail::group_sum_c<16>(sum);
+            if ((c8 & 15) == 0) hsum[r * nspan + (c8 >> 4)] = sum;
+        }
+    }
+    __syncthreads();
+
+    // consume: per unit, A row n16 = token n16's slot of the expert (or zeros); D rows 4g + v = tokens
+    float yacc[4] = {0.f, 0.f, 0.f, 0.f};
+    int cc = 0, ci = 0;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint16_t *a_row = zero_block;
+    int64_t a_step = 0;
+    int sv[4] = {-1, -1, -1, -1};  // the slots of D rows 4g + v under the current unit
+    auto unit_begin = [&]() {
+        const int u = wave + ci * kWaves;
+        const int sa = R.slot_tab[u][n16];
+        a_row = sa >= 0 ? hs + sa * ldh + g * 32 : zero_block;
+        a_step = sa >= 0 ? kSpan : 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            sv[v] = R.slot_tab[u][4 * g + v];
+        }
+    };
+    if (groups > 0) unit_begin();
+    auto consume = [&](int gr, auto slot_tag) {
+        constexpr int RS = decltype(slot_tag)::value;
+        const uint4 sw = sw_n[RS], mw = mw_n[RS];
+        if (gr + kRing < groups) advance_issue();
+        issue_window(sw_n[RS], mw_n[RS]);
+        const uint16_t *ab = a_row + cc * a_step;
+#pragma unroll
+        for (int s = 0; s < kPrefetch; ++s) {
+            const uint4 w_cur = ring[RS][s];
+            issue_slot(ring[RS], s);
+            f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8 *>(ab + s * a_step + t * 8);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, qmm::detail::codes_b<4>(w_cur, t), D, 0, 0, 0);
+            }
+            const uint32_t swd = qmm::detail::dword(sw, s >> 1), mwd = qmm::detail::dword(mw, s >> 1);
+            const float s_ = __uint_as_float((s & 1) ? (swd & 0xFFFF0000u) : (swd << 16));
+            const float m_ = __uint_as_float((s & 1) ? (mwd & 0xFFFF0000u) : (mwd << 16));
+            const float cm = fmaf(-128.f, s_, m_);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float xv = sv[v] >= 0 ? hsum[sv[v] * nspan + cc + s] : 0.f;
+                acc[v] = fmaf(s_, D[v], fmaf(cm, xv, acc[v]));
+            }
+        }
+        if (gr >= groups) return;  // the phantom group
+        if (cc + SPG < nspan) {
+            cc += SPG;
+            return;
+        }
+        cc = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            if (sv[v] >= 0) yacc[v] = fmaf(R.coef[sv[v]], acc[v], yacc[v]);
+        acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (++ci < my) unit_begin();
+    };
+    // Runs of kRing groups, all issuing their loads (a count short of a multiple of kRing ends with phantom groups
+    // that re-load the last one and stop after their MFMAs): a consume whose loads were conditional would merge two
+    // versions of the ring registers, and the copies at such a merge wait for every outstanding load.
+    for (int gr = 0; gr < groups; gr += kRing) {
+        consume(gr, std::integral_constant<int, 0>{});
+        consume(gr + 1, std::integral_constant<int, 1>{});
+    }
+
+    // the waves' sums in wave order; tokens with an invalid slot get NaN rows (the combine's rule)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave][4 * g + v][n16] = yacc[v];
+    __syncthreads();
+    if (tid < M * 16) {
+        const int m = tid >> 4, c = tid & 15;
+        const int64_t n = n0 + c;
+        float y = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) y += red[w][m][c];
+        bool bad = false;
+        for (int a = 0; a < A; ++a) bad |= (bad_slots >> (m * A + a)) & 1ull;
+        if (bad) y = qnan();
+        if (n < N) {
+            if (p.act == SX_ACT_F32) static_cast<float *>(p.y)[(int64_t)m * N + n] = y;
+            else static_cast<uint16_t *>(p.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16(y);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gate_up(const GateUpParams &p, int cus, hipStream_t stream) {
+    const int n_items = p.M * (int)(p.K / 8);
+    const int nb = (n_items + kThreads - 1) / kThreads;
+    const int nv = p.E <= 256 ? 4 : p.E <= 512 ? 8 : 16;
+    const dim3 grid((unsigned)cus);
+    auto go = [&](auto nv_tag, auto nb_tag) {
+        gate_up_kernel<decltype(nv_tag)::value, decltype(nb_tag)::value><<<grid, kThreads, 0, stream>>>(p);
+    };
+    auto by_nb = [&](auto nv_tag) {
+        if (nb <= 4) go(nv_tag, std::integral_constant<int, 4>{});
+        else if (nb <= 8) go(nv_tag, std::integral_constant<int, 8>{});
+        else go(nv_tag, std::integral_constant<int, 16>{});
+    };
+    if (nv == 4) by_nb(std::integral_constant<int, 4>{});
+    else if (nv == 8) by_nb(std::integral_constant<int, 8>{});
+    else by_nb(std::integral_constant<int, 16>{});
+    return hipGetLastError();
+}
+
+hipError_t launch_down(const DownParams &p, hipStream_t stream) {
+    const int n_items = p.M * p.A * (int)(p.K / 8);
+    const int nb = (n_items + kThreads - 1) / kThreads;
+    const dim3 grid((unsigned)((p.N + 15) / 16));
+    if (nb <= 4) down_kernel<4><<<grid, kThreads, 0, stream>>>(p);
+    else if (nb <= 8) down_kernel<8><<<grid, kThreads, 0, stream>>>(p);
+    else down_kernel<16><<<grid, kThreads, 0, stream>>>(p);
+    return hipGetLastError();
+}
+
+}  // namespace sx::vf
+
+using namespace sx;
+
+namespace {
+
+// The fused path's shape limits (all of them hold for the MTP verify layer: M <= 16, K = 4096, I = 1024).
+int check_gate_up(const char *fn, int64_t M, int64_t A, int64_t E, int64_t k, int64_t Ew, const sx_qview *w, int act) {
+    SX_CHECK(w != nullptr && w->q != nullptr && w->scale != nullptr && w->minv != nullptr, fn, " null weight view");
+    SX_CHECK(act == SX_ACT_BF16, fn, " activations must be BF16 (got ", act, ")");
+    SX_CHECK(M >= 1 && M <= vf::kMaxTokens && M * A <= vf::kMaxSlots, fn, " M = ", M, ", A = ", A, ": needs M <= ",
+             vf::kMaxTokens, " and M * A <= ", vf::kMaxSlots);
+    SX_CHECK(E >= 1 && k >= 1 && k <= E && Ew >= 1 && Ew <= vf::kMaxExperts, fn, " E = ", E, ", k = ", k, ", Ew = ", Ew);
+    SX_CHECK(w->G == 128 && w->N % Ew == 0 && (w->N / Ew) % 2 == 0, fn, " gate_up view N = ", w->N, ", G = ", w->G,
+             ": needs G = 128 and N a multiple of 2 Ew");
+    const int64_t K = w->K;
+    SX_CHECK((K == 512 || K == 1024 || K == 2048 || K == 4096) && M * (K + 8) <= vf::kXsElems, fn, " K = ", K,
+             " with M = ", M, " does not fit the fused kernel");
+    SX_CHECK(aligned(w->scale, 8) && aligned(w->minv, 8) && aligned(w->q, 16), fn, " weight arrays misaligned");
+    return SX_OK;
+}
+
+int check_down(const char *fn, int64_t M, int64_t A, int64_t Ew, const sx_qview *w, int act) {
+    SX_CHECK(w != nullptr && w->q != nullptr && w->scale != nullptr && w->minv != nullptr, fn, " null weight view");
+    SX_CHECK(act == SX_ACT_BF16, fn, " activations must be BF16 (got ", act, ")");
+    SX_CHECK(M >= 1 && M <= vf::kMaxTokens && A >= 1 && M * A <= vf::kMaxSlots, fn, " M = ", M, ", A = ", A,
+             ": needs M <= ", vf::kMaxTokens, " and M * A <= ", vf::kMaxSlots);
+    SX_CHECK(Ew >= 1 && Ew <= vf::kMaxExperts && w->N % Ew == 0, fn, " Ew = ", Ew, ", down view N = ", w->N);
+    const int64_t K = w->K;
+    SX_CHECK(w->G == 128 && (K == 1024 || K == 2048) && M * A * (K + 8) <= vf::kHsElems, fn, " K = ", K, ", G = ",
+             w->G, " with M * A = ", M * A, " does not fit the fused kernel");
+    SX_CHECK(aligned(w->scale, 16) && aligned(w->minv, 16) && aligned(w->q, 16), fn, " weight arrays misaligned");
+    return SX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sx_moe_verify_supported(int64_t M, int64_t A, int64_t E, int64_t k, int64_t Ew, const sx_qview *gate_up,
+                            const sx_qview *down, int act) {
+    if (int rc = check_gate_up("sx_moe_verify_supported", M, A, E, k, Ew, gate_up, act)) return rc;
+    if (int rc = check_down("sx_moe_verify_supported", M, A, Ew, down, act)) return rc;
+    SX_CHECK(down->K == gate_up->N / Ew / 2, "down K = ", down->K, " is not the gate_up I = ", gate_up->N / Ew / 2);
+    return SX_OK;
+}
+
+int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
+                          const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *w, int64_t Ew,
+                          int32_t *ids, float *coef, void *h, int act, uint32_t *router_err, uint32_t *expert_err,
+                          sx_stream stream) {
+    const char *fn = "sx_moe_verify_gate_up";
+    const int64_t A = k + (shared_logit ? 1 : 0);
+    SX_CHECK(x != nullptr && logits != nullptr && ids != nullptr && coef != nullptr && h != nullptr &&
+                 router_err != nullptr && expert_err != nullptr,
+             fn, " null pointer");
+    if (int rc = check_gate_up(fn, M, A, E, k, Ew, w, act)) return rc;
+    SX_CHECK(ld >= E && (shared_logit == nullptr || shared_ld >= 1), fn, " ld = ", ld, ", shared_ld = ", shared_ld);
+    SX_CHECK(aligned(x, 16) && aligned(h, 2), fn, " x must be 16-byte aligned");
+    const int64_t I = w->N / Ew / 2;
+    SX_CHECK(apart(h, M * A * I * 2, x, M * w->K * 2), fn, " h overlaps x");
+    vf::GateUpParams p{};
+    p.x = static_cast<const uint16_t *>(x), p.M = (int)M, p.A = (int)A, p.k = (int)k, p.E = (int)E, p.Ew = (int)Ew;
+    p.logits = logits, p.ld = ld, p.shared_logit = shared_logit, p.shared_ld = shared_ld, p.shared_id = shared_id;
+    p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = w->N / Ew, p.K = w->K;
+    p.ids = ids, p.coef = coef, p.h = static_cast<uint16_t *>(h), p.router_err = router_err, p.expert_err = expert_err;
+    SX_HIP(vf::launch_gate_up(p, device_cus(), stream_of(stream)), fn);
+    return SX_OK;
+}
+
+int sx_moe_verify_down(const void *h, int64_t M, int64_t A, const int32_t *ids, const float *coef, const sx_qview *w,
+                       int64_t Ew, void *y, int act, uint32_t *expert_err, sx_stream stream) {
+    const char *fn = "sx_moe_verify_down";
+    SX_CHECK(h != nullptr && ids != nullptr && coef != nullptr && y != nullptr && expert_err != nullptr, fn,
+             " null pointer");
+    if (int rc = check_down(fn, M, A, Ew, w, act)) return rc;
+    SX_CHECK(aligned(h, 16), fn, " h must be 16-byte aligned");
+    const int64_t N = w->N / Ew;
+    SX_CHECK(apart(y, M * N * 2, h, M * A * w->K * 2), fn, " y overlaps h");
+    vf::DownParams p{};
+    p.h = static_cast<const uint16_t *>(h), p.M = (int)M, p.A = (int)A, p.Ew = (int)Ew, p.ids = ids, p.coef = coef;
+    p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = N, p.K = w->K, p.y = y, p.act = act;
+    p.expert_err = expert_err;
+    SX_HIP(vf::launch_down(p, stream_of(stream)), fn);
+    return SX_OK;
+}
+
+}  // extern "C"

@@ -126,6 +126,42 @@ def router_group(logits, E, k, ws=None, ids=None, coef=None, router_err=None, ex
     return ids, coef, ws, router_err, expert_err
 
 
+def verify_supported(M, A, E, k, Ew, gate_up, down, act=ACT_BF16):
+    """Whether the two-launch verify FFN (verify_gate_up + verify_down) takes this shape."""
+    return lib().sx_moe_verify_supported(M, A, E, k, Ew, gate_up.view(), down.view(), act) == 0
+
+
+def verify_gate_up(x, logits, w, E, k, Ew=None, shared_logit=None, shared_id=0, ids=None, coef=None, h=None,
+                   router_err=None, expert_err=None, stream=None):
+    """moe_router + gather_swiglu in one launch at verify width: ids, coef [M, A], h [M, A, I]."""
+    M, ld = x.shape[0], logits.stride(0)
+    Ew = E if Ew is None else Ew
+    A = k + (shared_logit is not None)
+    I = w.N // Ew // 2
+    dev = x.device
+    ids = torch.empty((M, A), dtype=torch.int32, device=dev) if ids is None else ids
+    coef = torch.empty((M, A), dtype=torch.float32, device=dev) if coef is None else coef
+    h = torch.empty((M, A, I), dtype=x.dtype, device=dev) if h is None else h
+    router_err = _err(dev) if router_err is None else router_err
+    expert_err = _err(dev) if expert_err is None else expert_err
+    sld = 0 if shared_logit is None else shared_logit.stride(0)
+    check(lib().sx_moe_verify_gate_up(_p(x), M, _p(logits), ld, E, k, _p(shared_logit), sld, shared_id, w.view(), Ew,
+                                      _p(ids), _p(coef), _p(h), act_of(x), _p(router_err), _p(expert_err),
+                                      _s(stream)))
+    return ids, coef, h, router_err, expert_err
+
+
+def verify_down(h, w, ids, coef, Ew, y=None, expert_err=None, stream=None):
+    """y[M, N] = sum_a coef[m, a] * (h[m, a] . W[ids[m, a]]) in one launch at verify width."""
+    M, A = ids.shape
+    N = w.N // Ew
+    y = torch.empty((M, N), dtype=h.dtype, device=h.device) if y is None else y
+    expert_err = _err(h.device) if expert_err is None else expert_err
+    check(lib().sx_moe_verify_down(_p(h), M, A, _p(ids), _p(coef), w.view(), Ew, _p(y), act_of(h), _p(expert_err),
+                                   _s(stream)))
+    return y, expert_err
+
+
 def group_routes(ids, E, ws=None, err=None, stream=None):
     M, A = ids.shape
     nb = route_workspace_bytes(M, A, E)
