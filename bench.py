@@ -60,6 +60,17 @@ def time_launches(fn, n, warm=5):
     return a.elapsed_time(b) / n
 
 
+def gate_up_bytes(U, per_expert, M, d, E, k, I):
+    """Algorithmic bytes of one routing + gate_up launch: the U distinct experts' gate_up rows (codes, scales,
+    mins), the activations and router logits read, ids / coef and the SwiGLU output written."""
+    return U * per_expert + M * d * 2 + M * E * 4 + M * k * (4 + 4) + M * k * I * 2
+
+
+def down_bytes(U, per_expert, M, d, k, I):
+    """Algorithmic bytes of one down + combine launch: the U experts' down rows, h and the routing read, y written."""
+    return U * per_expert + M * k * I * 2 + M * k * (4 + 4) + M * d * 2
+
+
 def moe_layer_bench(args, out):
     import numpy as np
     import torch
@@ -83,7 +94,7 @@ def moe_layer_bench(args, out):
         layer.forward(xs[r])
         ids = layer.ids.clone()
         ws, _ = kx.group_routes(ids, E)
-        routes.append((ids, layer.coef.clone(), ws))
+        routes.append((ids, layer.coef.clone(), ws, layer.logits.clone()))
         U = int(torch.unique(ids).numel())
         Us.append(U)
         bytes_layer.append(U * per_expert + Wr.numel() * 4 + 2 * M * d * 2)
@@ -111,16 +122,19 @@ def moe_layer_bench(args, out):
     out["distinct_experts_mean"] = round(sum(Us) / R, 2)
     out["wall_s"] = round(wall, 3)
 
-    # dominant kernel alone: grouped gate_up + SwiGLU over the same rotating routes
+    # dominant kernel alone: routing + gate_up + SwiGLU (the layer's second launch) over the same rotating batches
     h = torch.empty((M, k, I), dtype=torch.bfloat16, device="cuda")
+    ids_b = torch.empty((M, k), dtype=torch.int32, device="cuda")
+    coef_b = torch.empty((M, k), dtype=torch.float32, device="cuda")
+    rerr, eerr = torch.zeros(4, dtype=torch.int32, device="cuda"), torch.zeros(4, dtype=torch.int32, device="cuda")
 
     def gate_up(i):
-        ids, coef, ws = routes[i % R]
-        kx.gather_grouped(xs[i % R], gu, E, ws, M, k, swiglu=True, y=h)
+        kx.verify_gate_up(xs[i % R], routes[i % R][3], gu, E, k, ids=ids_b, coef=coef_b, h=h, router_err=rerr,
+                          expert_err=eerr)
 
     n = max(args.steps, 64)
     ms = time_launches(gate_up, n)
-    gu_bytes = sum(Us[i % R] * gu_per_expert + M * d * 2 + M * k * I * 2 for i in range(n)) / n
+    gu_bytes = sum(gate_up_bytes(Us[i % R], gu_per_expert, M, d, E, k, I) for i in range(n)) / n
     achieved = gu_bytes / (ms * 1e-3) / 1e9
     traffic = None
     tj = os.path.join(ROOT, TRAFFIC_JSON)
@@ -129,20 +143,18 @@ def moe_layer_bench(args, out):
             traffic = json.load(f).get("gate_up", {}).get("hbm_bytes_per_launch")
     out["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                       "kernel": "qmm_kernel SWIGLU (grouped gate_up + SwiGLU)", "avg_launch_us": round(ms * 1e3, 3),
+                       "kernel": "gate_up_kernel (routing + gate_up + SwiGLU)", "avg_launch_us": round(ms * 1e3, 3),
                        "algorithmic_bytes_per_launch": int(gu_bytes)}
 
-    # the down projection + combine, alone
+    # the down projection + combine (the layer's third launch), alone
     hh = [torch.randn((M, k, I), device="cuda").to(torch.bfloat16) for _ in range(R)]
     yb = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
-    part = torch.empty((M * k, d), dtype=torch.float32, device="cuda")
 
     def down(i):
-        ids, coef, ws = routes[i % R]
-        kx.combine_grouped(hh[i % R], dn, E, ids, coef, ws, partial=part, y=yb)
+        kx.verify_down(hh[i % R], dn, routes[i % R][0], routes[i % R][1], E, y=yb, expert_err=eerr)
 
     ms_dn = time_launches(down, n)
-    dn_bytes = sum(Us[i % R] * (dn.nbytes() // E) for i in range(n)) / n
+    dn_bytes = sum(down_bytes(Us[i % R], dn.nbytes() // E, M, d, k, I) for i in range(n)) / n
     out["down_combine"] = {"avg_us": round(ms_dn * 1e3, 3), "GBps": round(dn_bytes / (ms_dn * 1e-3) / 1e9, 1)}
     return layer, xs, routes
 
@@ -289,7 +301,8 @@ def extra_configs(out):
 
 def probe():
     """A plain copy kernel of known size (read COPY_PROBE_BYTES, write COPY_PROBE_BYTES), then the config-3 gate_up
-    and down kernels alone over the rotating routes. Run under rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE)."""
+    (routing + gate_up + SwiGLU) and down (+ combine) kernels alone over the rotating batches. Run under rocprofv3
+    --pmc FETCH_SIZE (then WRITE_SIZE)."""
     import torch
 
     from strixite_amd import kernels as kx
@@ -311,20 +324,20 @@ def probe():
     routes, Us = [], []
     for r in range(R):
         layer.forward(xs[r])
-        ids = layer.ids.clone()
-        routes.append((ids, layer.coef.clone(), kx.group_routes(ids, E)[0]))
-        Us.append(int(torch.unique(ids).numel()))
+        routes.append((layer.ids.clone(), layer.coef.clone(), layer.logits.clone()))
+        Us.append(int(torch.unique(routes[-1][0]).numel()))
     h = torch.empty((M, k, I), dtype=torch.bfloat16, device="cuda")
+    ids_b = torch.empty((M, k), dtype=torch.int32, device="cuda")
+    coef_b = torch.empty((M, k), dtype=torch.float32, device="cuda")
     yb = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
-    part = torch.empty((M * k, d), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     for i in range(R):
-        kx.gather_grouped(xs[i], gu, E, routes[i][2], M, k, swiglu=True, y=h)
+        kx.verify_gate_up(xs[i], routes[i][2], gu, E, k, ids=ids_b, coef=coef_b, h=h)
     for i in range(R):
-        kx.combine_grouped(h, dn, E, routes[i][0], routes[i][1], routes[i][2], partial=part, y=yb)
+        kx.verify_down(h, dn, routes[i][0], routes[i][1], E, y=yb)
     torch.cuda.synchronize()
-    alg = {"gate_up": sum(U * (gu.nbytes() // E) + M * d * 2 + M * k * I * 2 for U in Us) / R,
-           "down": sum(U * (dn.nbytes() // E) + M * k * I * 2 + M * k * d * 4 for U in Us) / R}
+    alg = {"gate_up": sum(gate_up_bytes(U, gu.nbytes() // E, M, d, E, k, I) for U in Us) / R,
+           "down": sum(down_bytes(U, dn.nbytes() // E, M, d, k, I) for U in Us) / R}
     print(json.dumps({"probe": "done", "algorithmic_bytes_per_launch": alg, "distinct_experts": Us}))
 
 
@@ -343,7 +356,7 @@ def pmc_summary(fetch_dir, write_dir):
                 name, v = r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0  # KiB -> bytes
                 if "MulFunctor" in name:
                     copies.append((int(r["Grid_Size"]), v))
-                key = "gate_up" if "qmm_kernel<4, 1, 2," in name else "down" if "qmm_kernel<4, 1, 3," in name else None
+                key = "gate_up" if "gate_up_kernel" in name else "down" if "down_kernel" in name else None
                 if key:
                     rows.setdefault(key, []).append(v)
         big = max(g for g, _ in copies)  # the copy probe: the largest multiply launched
