@@ -2,37 +2,36 @@
 //
 // The verify kernel (qmm) stages every activation row of a unit over the whole K in LDS and passes the weights once
 // per 16 rows; with hundreds of rows a bucket (kernels/moe_grouped.hpp:5-17: the prefill path) that re-streams each
-// expert's weights per 16 rows. Here a block owns a 64-slot tile of one bucket (the workspace's wide tiles,
-// moe_grouped.hip:63-81) times 256 weight rows (8 waves x 2 tiles of 16; SwiGLU: 128 features, gate and up), and
-// walks K one span (128 codes, one quantization group) a step through a 4-stage pipeline of direct global->LDS
-// loads (DMA): the block's activation rows (swizzled so that the MFMA operand reads are conflict-free) and each
-// wave's weight codes (16 rows x 64 B a tile, in the MFMA B layout, as in qmm), scales and mins, three steps ahead.
-// A code fragment feeds 4 token blocks of 16 slots each, and each weight tile is read once a 64-slot tile (the
-// other tiles of the same bucket run next to it and find it in L2). Per span:
-//   acc[token][row] += s[row] * D + (m[row] - 128 s[row]) * sum_span x[token]
-// with D = sum x * (128 + code) exactly from v_mfma_f32_16x16x32_bf16 (the same identity as qmm).
-// Epilogues: SwiGLU (gate and up tiles of the same 16 features in one wave), plain gather, FP32 partials (combine).
+// expert's weights per 16 rows. Here a block (4 waves, two blocks a CU) owns a 64-slot tile of one bucket (the
+// workspace's wide tiles, moe_grouped.hip:63-81) times 256 weight rows; a wave owns all 64 slots times 64 rows (two
+// 32-row tiles; SwiGLU: the gate and the up rows of 32 features) as 2 x 2 v_mfma_f32_32x32x16_bf16 tiles, so each
+// activation fragment read from LDS feeds two MFMAs and each weight fragment two. K advances one span (128 codes =
+// one quantization group) a step:
+//   - the block's 64 activation rows of the span arrive by direct global->LDS loads (DMA) into a 4-stage ring,
+//     three steps ahead, each row's sixteen 16-byte chunks XOR-swizzled so that the MFMA operand reads are free of
+//     bank conflicts; the block sums each row's span one step ahead of its use;
+//   - each lane loads its weight rows' codes (32 bytes a row a span) and scales straight into registers, two steps
+//     ahead, and turns a dword of codes into the BF16 operand (128 + code) with four byte selects;
+//   - per span: acc[slot][row] += s[row] * D + (m[row] - 128 s[row]) * sum_span x[slot], with D = the span's
+//     sum x * (128 + code) from the MFMAs, exact in FP32 (the identity qmm uses).
+// MFMA k order: lane half h, MFMA kk, element e of a span <-> code h * 64 + kk * 8 + e (any order A and B share).
+// Epilogues: SwiGLU (gate and up of the same features in one wave), plain gather, FP32 partials (combine).
 #include "gemm_grouped.hpp"
 #include "qmm_impl.hpp"
 
 namespace sx::gg {
 namespace {
 
-using qmm::detail::bf16x8;
-using qmm::detail::f32x4;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 512, kWaves = 8;
+constexpr int kThreads = 256, kWaves = 4;
 constexpr int kBM = 64;                      // slots a block tile
 constexpr int kSpan = 128, kSpanBytes = 64;  // q4 codes / bytes a span (= one G = 128 group) = one K step
-constexpr int kUnits = kSpan / 8;            // 16-byte units of a row a K step (16)
-constexpr int kStages = 4;                   // K steps in LDS: three in flight while one is computed
-constexpr int kTW = 2;                       // 16-row weight tiles a wave
-constexpr int kXInstr = kBM * kUnits / 64 / kWaves;  // activation DMA instructions a wave a step (2)
-constexpr int kLoadsOdd = kXInstr + kTW;        // activation + code DMA instructions a wave an odd step (4)
-constexpr int kLoadsEven = kLoadsOdd + 2 * kTW;  // even steps add the scale and min words of two groups (8)
-constexpr int kXBytes = kBM * kUnits * 16;             // 16 KB
-constexpr int kWBytes = kWaves * kTW * 64 * 16;        // 16 KB: a wave's tiles, lane-ordered
-constexpr int kSBytes = kWaves * kTW * 2 * 64 * 4;     // 8 KB: scale / min words, lane-ordered
+constexpr int kStages = 4;                   // activation stages in LDS: three in flight while one is read
+constexpr int kStageBytes = kBM * kSpan * 2;  // 16 KB
+constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 16-byte-a-lane DMA instructions a wave a step (4)
+constexpr int kLoadsPerStep = kDmaPerWave + 8;  // + 4 code loads (2 rows x 2 halves) + 4 scale / min loads
 
 struct Params {
     const uint16_t *x;  // BF16 activations [tokens or slots, K]
@@ -42,12 +41,21 @@ struct Params {
     const int32_t *ws;
     int64_t A, N, K;  // slots a token; rows an expert (SWIGLU: 2I); K
     int64_t E;
+    int nrb;  // row blocks
 };
 
-// B operand of MFMA c from a lane's 16 code bytes in natural code order: dword c's nibbles j = 0..7 (codes
-// k0 + j, the low nibble the even code) as BF16 128 + code, pairs assembled by byte selects.
-__device__ __forceinline__ bf16x8 codes_nat(const uint4 &w, int c) {
-    const uint32_t d = qmm::detail::dword(w, c), lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+// The 1-D grid in groups of 8 tiles x nrb row blocks, row-block-major inside a group: the row blocks of a tile get
+// block ids of one residue mod 8 - the same XCD under the round-robin dispatch - close together, so the tile's
+// activation rows come from HBM once and from that XCD's L2 for the other row blocks.
+__device__ __forceinline__ int tile_of(unsigned id, int nrb) {
+    const unsigned grp = id / (8u * nrb), r = id % (8u * nrb);
+    return (int)(grp * 8 + r % 8);
+}
+__device__ __forceinline__ int rowblock_of(unsigned id, int nrb) { return (int)((id % (8u * nrb)) / 8); }
+
+// Operand of 8 codes (one dword: the low nibble of byte b is code 2b) in natural order as BF16 128 + code.
+__device__ __forceinline__ bf16x8 codes_nat(uint32_t d) {
+    const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
     uint4 v;
     v.x = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x43004300u;
     v.y = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x43004300u;
@@ -59,24 +67,19 @@ __device__ __forceinline__ bf16x8 codes_nat(const uint4 &w, int c) {
 __device__ __forceinline__ void dma16(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
 }
-__device__ __forceinline__ void dma4(const void *src, void *lds) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
-}
 
 template <int MODE, typename TY>
-__global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
-    // One array a stage and kind, so that the wait-count pass tells a stage's DMA apart from the others'.
-    __shared__ __attribute__((aligned(16))) unsigned char x0[kXBytes], x1[kXBytes], x2[kXBytes], x3[kXBytes];
-    __shared__ __attribute__((aligned(16))) unsigned char w0[kWBytes], w1[kWBytes], w2[kWBytes], w3[kWBytes];
-    // scale / min words (two groups each) load on even steps only; odd step k uses step k - 1's
-    __shared__ __attribute__((aligned(16))) unsigned char c0[kSBytes], c2[kSBytes];
-    __shared__ __attribute__((aligned(16))) float ss[kStages][kBM];
+__global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
+    // One array a stage, so that the wait-count pass tells a stage's DMA apart from the others'.
+    __shared__ __attribute__((aligned(16))) unsigned char x0[kStageBytes], x1[kStageBytes], x2[kStageBytes],
+        x3[kStageBytes];
+    __shared__ __attribute__((aligned(16))) float xsum[kStages][kBM];
     __shared__ int64_t s_xrow[kBM], s_out[kBM];
     __shared__ int s_T, s_bucket;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n16 = lane & 15, g = lane >> 4;
+    const int j = lane & 31, h = lane >> 5;  // MFMA row / column of the lane, its k half
     const int64_t K = p.K;
     const int E = (int)p.E;
 
@@ -85,7 +88,7 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
         const int32_t *ws = p.ws;
         const int32_t n_wt = ws[3], S = ws[1];
         int T = 0, bucket = -1;
-        const int u = (int)blockIdx.x;
+        const int u = tile_of(blockIdx.x, p.nrb);
         if (u < n_wt) {
             const int32_t *offsets = ws + 4, *slots = offsets + E + 2;
             const int64_t Tmax = (int64_t)S / 16 + E + 2, WTmax = (int64_t)S / 64 + E + 2;
@@ -105,8 +108,8 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
     const int T = __builtin_amdgcn_readfirstlane(s_T), bucket = __builtin_amdgcn_readfirstlane(s_bucket);
     if (T == 0) return;  // past the tile count: uniform for the block
     const int64_t Nrows = MODE == qmm::SWIGLU ? p.N / 2 : p.N;  // output rows (features) an expert
-    constexpr int kOutRows = MODE == qmm::SWIGLU ? kWaves * 16 : kWaves * kTW * 16;  // output rows a block
-    const int64_t r0 = (int64_t)blockIdx.y * kOutRows;
+    constexpr int kOutRows = MODE == qmm::SWIGLU ? kWaves * 32 : kWaves * 64;  // output rows a block
+    const int64_t r0 = (int64_t)rowblock_of(blockIdx.x, p.nrb) * kOutRows;
     if (bucket == E) {  // invalid ids (reported by the grouping): NaN rows, never an out-of-range weight read
         for (int i = tid; i < T * kOutRows; i += kThreads) {
             const int r = i / kOutRows;
@@ -117,172 +120,195 @@ __global__ void __launch_bounds__(kThreads) gg_kernel(Params p) {
         }
         return;
     }
+    if (tid >= T && tid < kBM) s_xrow[tid] = s_xrow[T - 1];  // rows past T: row T - 1 again, never stored
+    __syncthreads();
 
-    // ---- this lane's weight rows: tile t of the wave, row n16 (clamped into the expert; stores are masked) ----
-    const int64_t rowbytes = K / 2, ngroups = K / 128;
-    const uint8_t *qrow[kTW];
-    const uint32_t *srow[kTW], *mrow[kTW];  // the word holding groups 2i, 2i + 1
-    int64_t feat[kTW];
+    // ---- this lane's two weight rows (nb = 0, 1), clamped into the expert (stores are masked) ----
+    const int64_t rowbytes = K / 2, ngroups = K / kSpan;
+    const uint8_t *qrow[2];
+    const uint16_t *srow[2], *mrow[2];
+    int64_t feat[2];
 #pragma unroll
-    for (int t = 0; t < kTW; ++t) {
+    for (int nb = 0; nb < 2; ++nb) {
         int64_t n;  // row within the expert
-        if constexpr (MODE == qmm::SWIGLU) n = (t == 0 ? 0 : Nrows) + r0 + wave * 16 + n16;  // gate, up
-        else n = r0 + (wave * kTW + t) * 16 + n16;
-        feat[t] = MODE == qmm::SWIGLU ? r0 + wave * 16 + n16 : n;
+        if constexpr (MODE == qmm::SWIGLU) n = (nb == 0 ? 0 : Nrows) + r0 + wave * 32 + j;  // gate, up
+        else n = r0 + wave * 64 + nb * 32 + j;
+        feat[nb] = MODE == qmm::SWIGLU ? r0 + wave * 32 + j : n;
         const int64_t nn = min(n, (MODE == qmm::SWIGLU ? 2 * Nrows : Nrows) - 1);
         const int64_t row = (int64_t)bucket * p.N + nn;
-        qrow[t] = p.q + row * rowbytes + g * 16;
-        srow[t] = reinterpret_cast<const uint32_t *>(p.scale + row * ngroups);
-        mrow[t] = reinterpret_cast<const uint32_t *>(p.minv + row * ngroups);
+        qrow[nb] = p.q + row * rowbytes + h * 32;
+        srow[nb] = p.scale + row * ngroups;
+        mrow[nb] = p.minv + row * ngroups;
     }
-    // Activation staging: a step is 16 instructions of 64 lanes x 16 B; instruction I covers rows 4I .. 4I + 3,
-    // lane l = 16 (row % 4) + (chunk ^ row % 16), so each reads 4 x 256 contiguous bytes and the 16 rows an MFMA
-    // operand read touches fall in 16 different bank groups. This wave issues I = 2 wave + j (rows 8 wave + 4 j +
-    // lane / 16; past T: row T - 1 again, never stored).
-    const uint16_t *xl[kXInstr];
+    // Activation DMA: instruction I (0..15) covers tile rows 4I .. 4I + 3; lane l writes row 4I + l / 16, chunk
+    // (l & 15) ^ (row & 15), so slot s of a row holds chunk s ^ (row & 15). This wave issues I = 4 wave + i.
+    const uint16_t *xl[kDmaPerWave];
 #pragma unroll
-    for (int j = 0; j < kXInstr; ++j) {
-        const int r = 8 * wave + 4 * j + (lane >> 4);
-        xl[j] = p.x + s_xrow[min(r, T - 1)] + (((lane & 15) ^ (r & 15)) * 8);
+    for (int i = 0; i < kDmaPerWave; ++i) {
+        const int r = 4 * (kDmaPerWave * wave + i) + (lane >> 4);
+        xl[i] = p.x + s_xrow[r] + (((lane & 15) ^ (r & 15)) * 8);
     }
-
     auto xs_at = [&](int st) -> unsigned char * { return st == 0 ? x0 : st == 1 ? x1 : st == 2 ? x2 : x3; };
-    auto ws_at = [&](int st) -> unsigned char * { return st == 0 ? w0 : st == 1 ? w1 : st == 2 ? w2 : w3; };
-    auto cs_at = [&](int st) -> unsigned char * { return st < 2 ? c0 : c2; };  // stages 0, 1 share c0; 2, 3 c2
     const int nk = (int)(K / kSpan);
-    const int ntb = (T + 15) >> 4;  // 16-slot token blocks holding slots
+    const bool two_tb = T > 32;  // the second 32-slot half holds slots (uniform)
 
-    // K step k (clamped: past the end it re-loads the last step, never used), all by DMA into stage st: this wave's
-    // two activation instructions, its two code tiles (16 rows x 64 B, lane-ordered as the B operand wants them),
-    // and the scale / min words of its rows.
-    auto issue = [&](int kstep, int st) {  // st = kstep % kStages: even stages carry the scale words
+    // K step k (clamped: past the end it re-loads the last step, never used) into stage st
+    auto issue_x = [&](int kstep, int st) __attribute__((always_inline)) {
         const int k = min(kstep, nk - 1);
 #pragma unroll
-        for (int j = 0; j < kXInstr; ++j) dma16(xl[j] + (int64_t)k * kSpan, xs_at(st) + (2 * wave + j) * 1024);
-#pragma unroll
-        for (int t = 0; t < kTW; ++t) dma16(qrow[t] + (int64_t)k * kSpanBytes, ws_at(st) + (wave * kTW + t) * 1024);
-        if ((st & 1) == 0) {
-#pragma unroll
-            for (int t = 0; t < kTW; ++t) {
-                dma4(srow[t] + (k >> 1), cs_at(st) + ((wave * kTW + t) * 2 + 0) * 256);
-                dma4(mrow[t] + (k >> 1), cs_at(st) + ((wave * kTW + t) * 2 + 1) * 256);
-            }
-        }
+        for (int i = 0; i < kDmaPerWave; ++i)
+            dma16(xl[i] + (int64_t)k * kSpan, xs_at(st) + (kDmaPerWave * wave + i) * 1024);
     };
-    // Span sums: 8 threads a row, 2 units each (the swizzle only permutes a row's units), added across 8 lanes.
-    auto sum_spans = [&](int st) {
-        const int r = tid >> 3, part = tid & 7;
-        const unsigned char *xb = xs_at(st) + ((r >> 2) * 64 + (r & 3) * 16 + part * 2) * 16;
+    // the lane's codes (2 rows x 2 x 16 bytes) and scales / mins of step k, into a ring slot
+    uint4 cw[2][2][2];     // [ring slot][nb][half of the lane's 32 bytes]
+    uint32_t cs[2][2][2];  // [ring slot][nb][scale, min] as BF16 bits
+    auto issue_codes = [&](int kstep, uint4 (&w)[2][2], int half) {
+        const int k = min(kstep, nk - 1);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+            w[nb][half] = *reinterpret_cast<const uint4 *>(qrow[nb] + (int64_t)k * kSpanBytes + half * 16);
+    };
+    auto issue_scales = [&](int kstep, uint32_t (&s)[2][2]) {
+        const int k = min(kstep, nk - 1);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) s[nb][0] = srow[nb][k], s[nb][1] = mrow[nb][k];
+    };
+    // the span sums of stage st's 64 rows: 4 threads a row, 4 slots each (any slot order sums the row)
+    auto sum_rows = [&](int st) __attribute__((always_inline)) {
+        const int r = tid >> 2, qd = tid & 3;
+        const unsigned char *xb = xs_at(st) + r * 256 + qd * 64;
+        // read in asm: the wait-count pass would otherwise hold these reads for every DMA in flight (it cannot
+        // tell this stage from the one just issued); the step's barrier already covers this stage's DMA
+        const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)xb;
+        uint4 raw[4];
+        asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\tds_read_b128 %2, %4 offset:32\n\t"
+                     "ds_read_b128 %3, %4 offset:48\n\ts_waitcnt lgkmcnt(0)"
+                     : "=v"(raw[0]), "=v"(raw[1]), "=v"(raw[2]), "=v"(raw[3])
+                     : "v"(addr));
         float sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 4; ++i) {
             float v[8];
-            qmm::detail::unpack8(*reinterpret_cast<const uint4 *>(xb + i * 16), v);
+            qmm::detail::unpack8(raw[i], v);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) sum += v[j];
+            for (int e = 0; e < 8; ++e) sum += v[e];
         }
-        sum = qmm::detail::group_sum_c<8>(sum);
-        if (part == 0) ss[st][r] = sum;
+        sum = qmm::detail::group_sum_c<4>(sum);
+        if (qd == 0) xsum[st][r] = sum;
     };
 
-    f32x4 acc[kTW][4];
+    f32x16 acc[2][2];
 #pragma unroll
-    for (int t = 0; t < kTW; ++t)
+    for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) acc[t][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nb = 0; nb < 2; ++nb) acc[tb][nb] = f32x16{};
 
-    // Scale / min words of the current pair of steps: read from LDS on the even step and kept in registers for the
-    // odd one (by then the pair-after-next is already landing in the same array).
-    uint32_t swd[kTW], mwd[kTW];
-    auto compute = [&](auto st_tag) {
-        constexpr int st = decltype(st_tag)::value;
-        const unsigned char *xb = xs_at(st), *wb = ws_at(st), *cb = cs_at(st);
-        bf16x8 B[kTW][4];
-        float sc[kTW], cm[kTW];
+    // one K step on stage st with ring slot RS; the ring slot is re-loaded (step k + 2) as its codes are used
+    auto compute = [&](int k, int st, auto rs_tag) __attribute__((always_inline)) {
+        constexpr int RS = decltype(rs_tag)::value;
+        const unsigned char *xb = xs_at(st);
+        f32x16 D[2][2];
 #pragma unroll
-        for (int t = 0; t < kTW; ++t) {
-            const uint4 w = *reinterpret_cast<const uint4 *>(wb + (wave * kTW + t) * 1024 + lane * 16);
+        for (int half = 0; half < 2; ++half) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) B[t][c] = codes_nat(w, c);
-            if constexpr ((st & 1) == 0) {
-                swd[t] = *reinterpret_cast<const uint32_t *>(cb + ((wave * kTW + t) * 2 + 0) * 256 + lane * 4);
-                mwd[t] = *reinterpret_cast<const uint32_t *>(cb + ((wave * kTW + t) * 2 + 1) * 256 + lane * 4);
+            for (int kq = 0; kq < 4; ++kq) {
+                const int kk = half * 4 + kq;
+                bf16x8 bop[2];
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) bop[nb] = codes_nat(qmm::detail::dword(cw[RS][nb][half], kq));
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb) {
+                    if (tb == 1 && !two_tb) continue;
+                    const int row = tb * 32 + j;
+                    const bf16x8 aop =
+                        *reinterpret_cast<const bf16x8 *>(xb + row * 256 + (((h * 8 + kk) ^ (row & 15)) * 16));
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb)
+                        D[tb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop, bop[nb], kk == 0 ? f32x16{} : D[tb][nb],
+                                                                            0, 0, 0);
+                }
             }
-            sc[t] = __uint_as_float((st & 1) ? (swd[t] & 0xFFFF0000u) : (swd[t] << 16));
-            const float mv = __uint_as_float((st & 1) ? (mwd[t] & 0xFFFF0000u) : (mwd[t] << 16));
-            cm[t] = fmaf(-128.f, sc[t], mv);
+            issue_codes(k + 2, cw[RS], half);  // this half's codes are in the operands
         }
+        // fold the span: s * D + (m - 128 s) * xsum; a lane's value v is slot 8 (v / 4) + 4 h + v % 4 of its tile
+        float s_[2], cm[2];
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-            if (tb >= ntb) break;  // token blocks past the tile's slots (uniform)
-            const int r = tb * 16 + n16;
-            const unsigned char *xa = xb + ((r >> 2) * 64 + (r & 3) * 16) * 16;
-            bf16x8 Aop[4];
+        for (int nb = 0; nb < 2; ++nb) {
+            s_[nb] = bf16_to_f32(cs[RS][nb][0]);
+            cm[nb] = fmaf(-128.f, s_[nb], bf16_to_f32(cs[RS][nb][1]));
+        }
+        issue_scales(k + 2, cs[RS]);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) Aop[c] = *reinterpret_cast<const bf16x8 *>(xa + (((g * 4 + c) ^ n16) * 16));
-            const float4 xv = *reinterpret_cast<const float4 *>(&ss[st][tb * 16 + 4 * g]);
+        for (int tb = 0; tb < 2; ++tb) {
+            if (tb == 1 && !two_tb) continue;
 #pragma unroll
-            for (int t = 0; t < kTW; ++t) {
-                f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int vq = 0; vq < 4; ++vq) {
+                const float4 xv = *reinterpret_cast<const float4 *>(&xsum[st][tb * 32 + 8 * vq + 4 * h]);
+                const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-                for (int c = 0; c < 4; ++c) D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Aop[c], B[t][c], D, 0, 0, 0);
-                acc[t][tb][0] = fmaf(sc[t], D[0], fmaf(cm[t], xv.x, acc[t][tb][0]));
-                acc[t][tb][1] = fmaf(sc[t], D[1], fmaf(cm[t], xv.y, acc[t][tb][1]));
-                acc[t][tb][2] = fmaf(sc[t], D[2], fmaf(cm[t], xv.z, acc[t][tb][2]));
-                acc[t][tb][3] = fmaf(sc[t], D[3], fmaf(cm[t], xv.w, acc[t][tb][3]));
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb)
+                        acc[tb][nb][4 * vq + e] =
+                            fmaf(s_[nb], D[tb][nb][4 * vq + e], fmaf(cm[nb], xa[e], acc[tb][nb][4 * vq + e]));
             }
         }
     };
-    // One K step. Barriers are s_barrier with explicit waits (a __syncthreads() fence would wait for every
-    // outstanding DMA, the next steps' included). Step k's DMA of this wave has landed once only the three later
-    // issues are outstanding (VMEM completes in order); everyone's has after the barrier.
-    auto step = [&](int k, auto st_tag) {
+
+    // One K step k (stage k % 4, ring slot k % 2; both constants in the unrolled loop). A step issues kLoadsPerStep
+    // loads (4 DMA, then 8 register loads as the codes and scales are used); barriers are s_barrier with explicit
+    // waits (a __syncthreads() fence would wait for every outstanding load, the next steps' included).
+    //   wait: everything issued before the previous step has landed (DMA of step k + 1, codes of step k); barrier:
+    //   every wave is done with step k - 1 (stage (k + 3) % 4 is free) and sees the DMA of k + 1 and the sums of k.
+    auto step = [&](int k, auto st_tag, auto rs_tag) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_tag)::value;
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // everyone is done with step k - 1
-        issue(k + kStages - 1, (ST + kStages - 1) % kStages);
-        constexpr int kNewer = (ST & 1) ? 2 * kLoadsEven + kLoadsOdd : 2 * kLoadsOdd + kLoadsEven;  // issues k+1..k+3
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kNewer) : "memory");
-        sum_spans(ST);
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        compute(st_tag);
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kLoadsPerStep) : "memory");
+        issue_x(k + 3, (ST + 3) % kStages);
+        __builtin_amdgcn_sched_barrier(0);
+        sum_rows((ST + 1) % kStages);
+        compute(k, ST, rs_tag);
     };
 
-    static_assert(kStages % 2 == 0, "stage parity follows step parity");
+    // prologue: steps 0..2 of activations, 0..1 of weights, and the sums of step 0
 #pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue(s, s);
-    // unrolled by the stage count so that the stages are constants (a full unroll hoists every load and spills)
+    for (int s = 0; s < kStages - 1; ++s) issue_x(s, s);
+    issue_codes(0, cw[0], 0), issue_codes(0, cw[0], 1), issue_scales(0, cs[0]);
+    issue_codes(1, cw[1], 0), issue_codes(1, cw[1], 1), issue_scales(1, cs[1]);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the first steps landed everywhere
+    sum_rows(0);
+    // unrolled by the stage count (a multiple of the ring depth) so that stages and ring slots are constants
     for (int k = 0;; k += kStages) {
         if (k >= nk) break;
-        step(k, std::integral_constant<int, 0>{});
+        step(k, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
         if (k + 1 >= nk) break;
-        step(k + 1, std::integral_constant<int, 1>{});
+        step(k + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
         if (k + 2 >= nk) break;
-        step(k + 2, std::integral_constant<int, 2>{});
+        step(k + 2, std::integral_constant<int, 2>{}, std::integral_constant<int, 0>{});
         if (k + 3 >= nk) break;
-        step(k + 3, std::integral_constant<int, 3>{});
+        step(k + 3, std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{});
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped DMA past the end lands before the block exits
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the block exits
 
-    // ---- stores: D row = token block tb, rows 4g..4g+3; column = the lane's weight row ----
+    // ---- stores: tile (tb, nb), lane value v = slot tb * 32 + 8 (v / 4) + 4 h + v % 4, row j of the tile ----
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
+    for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int r = tb * 16 + 4 * g + v;
+        for (int v = 0; v < 16; ++v) {
+            const int r = tb * 32 + 8 * (v / 4) + 4 * h + v % 4;
             if (r >= T) continue;
             const int64_t o = s_out[r] * Nrows;
             if constexpr (MODE == qmm::SWIGLU) {
                 if (feat[0] < Nrows) {
-                    TY *h = static_cast<TY *>(p.y);
-                    const float gv = as_stored(acc[0][tb][v], h), uv = as_stored(acc[1][tb][v], h);
-                    store_act(h, o + feat[0], as_stored(silu(gv), h) * uv);
+                    TY *hy = static_cast<TY *>(p.y);
+                    const float gv = as_stored(acc[tb][0][v], hy), uv = as_stored(acc[tb][1][v], hy);
+                    store_act(hy, o + feat[0], as_stored(silu(gv), hy) * uv);
                 }
             } else {
 #pragma unroll
-                for (int t = 0; t < kTW; ++t) {
-                    if (feat[t] >= Nrows) continue;
-                    if constexpr (MODE == qmm::COMBINE) static_cast<float *>(p.y)[o + feat[t]] = acc[t][tb][v];
-                    else store_act(static_cast<TY *>(p.y), o + feat[t], acc[t][tb][v]);
+                for (int nb = 0; nb < 2; ++nb) {
+                    if (feat[nb] >= Nrows) continue;
+                    if constexpr (MODE == qmm::COMBINE) static_cast<float *>(p.y)[o + feat[nb]] = acc[tb][nb][v];
+                    else store_act(static_cast<TY *>(p.y), o + feat[nb], acc[tb][nb][v]);
                 }
             }
         }
@@ -297,7 +323,7 @@ hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
 }  // namespace
 
 bool eligible(int bits, int64_t G, int64_t K, int act) {
-    return bits == 4 && G == 128 && K % (2 * kSpan) == 0 && K >= 2 * kSpan && act == SX_ACT_BF16;
+    return bits == 4 && G == 128 && K % kSpan == 0 && K >= kSpan && act == SX_ACT_BF16;
 }
 
 hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int32_t *ws, int64_t M, int64_t A,
@@ -309,8 +335,9 @@ hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int
     const int64_t S = M * A;
     const int64_t wtiles = S / kBM + E + 2;  // WTmax: an upper bound of the 64-slot tiles; the rest exit at once
     const int64_t out_rows = mode == qmm::SWIGLU ? p.N / 2 : p.N;
-    const int64_t per_block = mode == qmm::SWIGLU ? kWaves * 16 : kWaves * kTW * 16;
-    const dim3 grid((unsigned)wtiles, (unsigned)((out_rows + per_block - 1) / per_block));
+    const int64_t per_block = mode == qmm::SWIGLU ? kWaves * 32 : kWaves * 64;
+    p.nrb = (int)((out_rows + per_block - 1) / per_block);
+    const dim3 grid((unsigned)((wtiles + 7) / 8 * 8 * p.nrb));
     hipError_t e;
     switch (mode) {
     case qmm::SWIGLU:
