@@ -31,7 +31,9 @@ constexpr int kSpan = 128, kSpanBytes = 64;  // q4 codes / bytes a span (= one G
 constexpr int kStages = 4;                   // activation stages in LDS: three in flight while one is read
 constexpr int kStageBytes = kBM * kSpan * 2;  // 16 KB
 constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 16-byte-a-lane DMA instructions a wave a step (4)
-constexpr int kLoadsPerStep = kDmaPerWave + 8;  // + 4 code loads (2 rows x 2 halves) + 4 scale / min loads
+constexpr int kLoadsPerStep = kDmaPerWave + 6;  // + 4 code loads (2 rows x 2 halves) + 2 scale loads
+constexpr int kMaxGroups = 32;  // K <= 4096: the span sums of every step stay in LDS
+constexpr int kSumStride = kMaxGroups + 4;  // floats a row (16-byte aligned, rows 4 banks apart)
 
 struct Params {
     const uint16_t *x;  // BF16 activations [tokens or slots, K]
@@ -73,7 +75,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     // One array a stage, so that the wait-count pass tells a stage's DMA apart from the others'.
     __shared__ __attribute__((aligned(16))) unsigned char x0[kStageBytes], x1[kStageBytes], x2[kStageBytes],
         x3[kStageBytes];
-    __shared__ __attribute__((aligned(16))) float xsum[kStages][kBM];
+    __shared__ __attribute__((aligned(16))) float xsum[kBM * kSumStride];  // [slot][span]
     __shared__ int64_t s_xrow[kBM], s_out[kBM];
     __shared__ int s_T, s_bucket;
 
@@ -161,20 +163,20 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     };
     // the lane's codes (2 rows x 2 x 16 bytes) and scales / mins of step k, into a ring slot
     uint4 cw[2][2][2];     // [ring slot][nb][half of the lane's 32 bytes]
-    uint32_t cs[2][2][2];  // [ring slot][nb][scale, min] as BF16 bits
+    uint32_t cs[2][2];  // [ring slot][nb]: the scale as BF16 bits (the mins are used once, at the end)
     auto issue_codes = [&](int kstep, uint4 (&w)[2][2], int half) {
         const int k = min(kstep, nk - 1);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
             w[nb][half] = *reinterpret_cast<const uint4 *>(qrow[nb] + (int64_t)k * kSpanBytes + half * 16);
     };
-    auto issue_scales = [&](int kstep, uint32_t (&s)[2][2]) {
+    auto issue_scales = [&](int kstep, uint32_t (&s)[2]) {
         const int k = min(kstep, nk - 1);
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) s[nb][0] = srow[nb][k], s[nb][1] = mrow[nb][k];
+        for (int nb = 0; nb < 2; ++nb) s[nb] = srow[nb][k];
     };
-    // the span sums of stage st's 64 rows: 4 threads a row, 4 slots each (any slot order sums the row)
-    auto sum_rows = [&](int st) __attribute__((always_inline)) {
+    // the span sums of stage st's 64 rows (K step grp): 4 threads a row, 4 slots each (any slot order sums the row)
+    auto sum_rows = [&](int st, int grp) __attribute__((always_inline)) {
         const int r = tid >> 2, qd = tid & 3;
         const unsigned char *xb = xs_at(st) + r * 256 + qd * 64;
         // read in asm: the wait-count pass would otherwise hold these reads for every DMA in flight (it cannot
@@ -194,7 +196,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
             for (int e = 0; e < 8; ++e) sum += v[e];
         }
         sum = qmm::detail::group_sum_c<4>(sum);
-        if (qd == 0) xsum[st][r] = sum;
+        if (qd == 0 && grp < nk) xsum[r * kSumStride + grp] = sum;
     };
 
     f32x16 acc[2][2];
@@ -230,28 +232,19 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
             }
             issue_codes(k + 2, cw[RS], half);  // this half's codes are in the operands
         }
-        // fold the span: s * D + (m - 128 s) * xsum; a lane's value v is slot 8 (v / 4) + 4 h + v % 4 of its tile
-        float s_[2], cm[2];
+        // fold the span: s * D (the (m - 128 s) * sum x term of every span is added once, at the end); a lane's
+        // value v is slot 8 (v / 4) + 4 h + v % 4 of its tile
+        float s_[2];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            s_[nb] = bf16_to_f32(cs[RS][nb][0]);
-            cm[nb] = fmaf(-128.f, s_[nb], bf16_to_f32(cs[RS][nb][1]));
-        }
+        for (int nb = 0; nb < 2; ++nb) s_[nb] = bf16_to_f32(cs[RS][nb]);
         issue_scales(k + 2, cs[RS]);
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             if (tb == 1 && !two_tb) continue;
 #pragma unroll
-            for (int vq = 0; vq < 4; ++vq) {
-                const float4 xv = *reinterpret_cast<const float4 *>(&xsum[st][tb * 32 + 8 * vq + 4 * h]);
-                const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+            for (int v = 0; v < 16; ++v)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-#pragma unroll
-                    for (int nb = 0; nb < 2; ++nb)
-                        acc[tb][nb][4 * vq + e] =
-                            fmaf(s_[nb], D[tb][nb][4 * vq + e], fmaf(cm[nb], xa[e], acc[tb][nb][4 * vq + e]));
-            }
+                for (int nb = 0; nb < 2; ++nb) acc[tb][nb][v] = fmaf(s_[nb], D[tb][nb][v], acc[tb][nb][v]);
         }
     };
 
@@ -265,7 +258,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kLoadsPerStep) : "memory");
         issue_x(k + 3, (ST + 3) % kStages);
         __builtin_amdgcn_sched_barrier(0);
-        sum_rows((ST + 1) % kStages);
+        sum_rows((ST + 1) % kStages, k + 1);
         compute(k, ST, rs_tag);
     };
 
@@ -275,7 +268,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     issue_codes(0, cw[0], 0), issue_codes(0, cw[0], 1), issue_scales(0, cs[0]);
     issue_codes(1, cw[1], 0), issue_codes(1, cw[1], 1), issue_scales(1, cs[1]);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the first steps landed everywhere
-    sum_rows(0);
+    sum_rows(0, 0);
     // unrolled by the stage count (a multiple of the ring depth) so that stages and ring slots are constants
     for (int k = 0;; k += kStages) {
         if (k >= nk) break;
@@ -288,6 +281,50 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         step(k + 3, std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{});
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the block exits
+
+    // ---- sum over the spans of (m - 128 s)[row] * sum x[slot], on the MFMA: 16 spans an instruction, both operands
+    // split into three BF16 terms (t0 = rne(v), t1 = rne(v - t0), t2 = rne(v - t0 - t1): 24 significant bits, as
+    // the FP32 fold this replaces; the term largely cancels s * 128 * sum x inside s * D, so 16 bits would not do).
+    // The six products down to 2^-16 of the whole; the rest (below 2^-24) are dropped. The sums of the last steps
+    // were written before the last step's barrier. ----
+    auto split3 = [](const float (&v)[8], bf16x8 (&t)[3]) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const __bf16 a = (__bf16)v[e];
+            const float r1 = v[e] - (float)a;
+            const __bf16 b = (__bf16)r1;
+            t[0][e] = a, t[1][e] = b, t[2][e] = (__bf16)(r1 - (float)b);
+        }
+    };
+    for (int g0 = 0; g0 < nk; g0 += 16) {
+        const int gl = g0 + h * 8;  // this lane's 8 spans
+        bf16x8 bt[2][3];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            float cmv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                cmv[e] = gl + e < nk ? fmaf(-128.f, bf16_to_f32(srow[nb][gl + e]), bf16_to_f32(mrow[nb][gl + e])) : 0.f;
+            split3(cmv, bt[nb]);
+        }
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            if (tb == 1 && !two_tb) continue;
+            float xv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[e] = gl + e < nk ? xsum[(tb * 32 + j) * kSumStride + gl + e] : 0.f;
+            bf16x8 at[3];
+            split3(xv, at);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                for (int pa = 0; pa < 3; ++pa)
+#pragma unroll
+                    for (int pb = 0; pb < 3 - pa; ++pb)  // (0,0) (0,1) (0,2) (1,0) (1,1) (2,0)
+                        acc[tb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(at[pa], bt[nb][pb], acc[tb][nb], 0, 0, 0);
+            }
+        }
+    }
 
     // ---- stores: tile (tb, nb), lane value v = slot tb * 32 + 8 (v / 4) + 4 h + v % 4, row j of the tile ----
 #pragma unroll
@@ -323,7 +360,7 @@ hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
 }  // namespace
 
 bool eligible(int bits, int64_t G, int64_t K, int act) {
-    return bits == 4 && G == 128 && K % kSpan == 0 && K >= kSpan && act == SX_ACT_BF16;
+    return bits == 4 && G == 128 && K % kSpan == 0 && K >= kSpan && K <= kSpan * kMaxGroups && act == SX_ACT_BF16;
 }
 
 hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int32_t *ws, int64_t M, int64_t A,
