@@ -206,8 +206,9 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         for (int nb = 0; nb < 2; ++nb) acc[tb][nb] = f32x16{};
 
     // one K step on stage st with ring slot RS; the ring slot is re-loaded (step k + 2) as its codes are used
-    auto compute = [&](int k, int st, auto rs_tag) __attribute__((always_inline)) {
+    auto compute = [&](int k, int st, auto rs_tag, auto two_tag) __attribute__((always_inline)) {
         constexpr int RS = decltype(rs_tag)::value;
+        constexpr bool TWO = decltype(two_tag)::value;  // the second 32-slot half holds slots
         const unsigned char *xb = xs_at(st);
         f32x16 D[2][2];
 #pragma unroll
@@ -220,7 +221,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
                 for (int nb = 0; nb < 2; ++nb) bop[nb] = codes_nat(qmm::detail::dword(cw[RS][nb][half], kq));
 #pragma unroll
                 for (int tb = 0; tb < 2; ++tb) {
-                    if (tb == 1 && !two_tb) continue;
+                    if (tb == 1 && !TWO) continue;
                     const int row = tb * 32 + j;
                     const bf16x8 aop =
                         *reinterpret_cast<const bf16x8 *>(xb + row * 256 + (((h * 8 + kk) ^ (row & 15)) * 16));
@@ -240,7 +241,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         issue_scales(k + 2, cs[RS]);
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
-            if (tb == 1 && !two_tb) continue;
+            if (tb == 1 && !TWO) continue;
 #pragma unroll
             for (int v = 0; v < 16; ++v)
 #pragma unroll
@@ -253,13 +254,13 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     // waits (a __syncthreads() fence would wait for every outstanding load, the next steps' included).
     //   wait: everything issued before the previous step has landed (DMA of step k + 1, codes of step k); barrier:
     //   every wave is done with step k - 1 (stage (k + 3) % 4 is free) and sees the DMA of k + 1 and the sums of k.
-    auto step = [&](int k, auto st_tag, auto rs_tag) __attribute__((always_inline)) {
+    auto step = [&](int k, auto st_tag, auto rs_tag, auto two_tag) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_tag)::value;
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kLoadsPerStep) : "memory");
         issue_x(k + 3, (ST + 3) % kStages);
         __builtin_amdgcn_sched_barrier(0);
         sum_rows((ST + 1) % kStages, k + 1);
-        compute(k, ST, rs_tag);
+        compute(k, ST, rs_tag, two_tag);
     };
 
     // prologue: steps 0..2 of activations, 0..1 of weights, and the sums of step 0
@@ -269,17 +270,22 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     issue_codes(1, cw[1], 0), issue_codes(1, cw[1], 1), issue_scales(1, cs[1]);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the first steps landed everywhere
     sum_rows(0, 0);
-    // unrolled by the stage count (a multiple of the ring depth) so that stages and ring slots are constants
-    for (int k = 0;; k += kStages) {
-        if (k >= nk) break;
-        step(k, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-        if (k + 1 >= nk) break;
-        step(k + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
-        if (k + 2 >= nk) break;
-        step(k + 2, std::integral_constant<int, 2>{}, std::integral_constant<int, 0>{});
-        if (k + 3 >= nk) break;
-        step(k + 3, std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{});
-    }
+    // unrolled by the stage count (a multiple of the ring depth) so that stages and ring slots are constants; one
+    // copy for tiles of more than 32 slots and one for the rest (no branch inside the K loop)
+    auto run = [&](auto two_tag) __attribute__((always_inline)) {
+        for (int k = 0;; k += kStages) {
+            if (k >= nk) break;
+            step(k, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, two_tag);
+            if (k + 1 >= nk) break;
+            step(k + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, two_tag);
+            if (k + 2 >= nk) break;
+            step(k + 2, std::integral_constant<int, 2>{}, std::integral_constant<int, 0>{}, two_tag);
+            if (k + 3 >= nk) break;
+            step(k + 3, std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{}, two_tag);
+        }
+    };
+    if (two_tb) run(std::true_type{});
+    else run(std::false_type{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the block exits
 
     // ---- sum over the spans of (m - 128 s)[row] * sum x[slot], on the MFMA: 16 spans an instruction, both operands
