@@ -211,24 +211,33 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         constexpr bool TWO = decltype(two_tag)::value;  // the second 32-slot half holds slots
         const unsigned char *xb = xs_at(st);
         f32x16 D[2][2];
+        // activation fragments one MFMA step ahead (their LDS latency hides behind the step before)
+        bf16x8 aop[2][2];  // [buffer][tb]
+        auto load_a = [&](int kk, bf16x8 (&a)[2]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                if (tb == 1 && !TWO) continue;
+                const int row = tb * 32 + j;
+                a[tb] = *reinterpret_cast<const bf16x8 *>(xb + row * 256 + (((h * 8 + kk) ^ (row & 15)) * 16));
+            }
+        };
+        load_a(0, aop[0]);
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
 #pragma unroll
             for (int kq = 0; kq < 4; ++kq) {
                 const int kk = half * 4 + kq;
+                if (kk < 7) load_a(kk + 1, aop[(kk + 1) & 1]);
                 bf16x8 bop[2];
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) bop[nb] = codes_nat(qmm::detail::dword(cw[RS][nb][half], kq));
 #pragma unroll
                 for (int tb = 0; tb < 2; ++tb) {
                     if (tb == 1 && !TWO) continue;
-                    const int row = tb * 32 + j;
-                    const bf16x8 aop =
-                        *reinterpret_cast<const bf16x8 *>(xb + row * 256 + (((h * 8 + kk) ^ (row & 15)) * 16));
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb)
-                        D[tb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop, bop[nb], kk == 0 ? f32x16{} : D[tb][nb],
-                                                                            0, 0, 0);
+                        D[tb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop[kk & 1][tb], bop[nb],
+                                                                            kk == 0 ? f32x16{} : D[tb][nb], 0, 0, 0);
                 }
             }
             issue_codes(k + 2, cw[RS], half);  // this half's codes are in the operands
