@@ -31,7 +31,8 @@ constexpr int kSpan = 128, kSpanBytes = 64;  // q4 codes / bytes a span (= one G
 constexpr int kStages = 4;                   // activation stages in LDS: three in flight while one is read
 constexpr int kStageBytes = kBM * kSpan * 2;  // 16 KB
 constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 16-byte-a-lane DMA instructions a wave a step (4)
-constexpr int kLoadsPerStep = kDmaPerWave + 6;  // + 4 code loads (2 rows x 2 halves) + 2 scale loads
+constexpr int kLoadsPerStep = kDmaPerWave + 6;  // most a step issues: + 4 code loads (2 rows x 2 halves)
+                                                // + 2 scale windows (every fourth step)
 constexpr int kMaxGroups = 32;  // K <= 4096: the span sums of every step stay in LDS
 constexpr int kSumStride = kMaxGroups + 4;  // floats a row (16-byte aligned, rows 4 banks apart)
 
@@ -163,17 +164,19 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     };
     // the lane's codes (2 rows x 2 x 16 bytes) and scales / mins of step k, into a ring slot
     uint4 cw[2][2][2];     // [ring slot][nb][half of the lane's 32 bytes]
-    uint32_t cs[2][2];  // [ring slot][nb]: the scale as BF16 bits (the mins are used once, at the end)
+    // the scales of 4 steps a row as one 8-byte window (fewer cache lines a step than one 2-byte load a step); the
+    // mins are used once, at the end
+    uint2 wcur[2], wnxt[2];
     auto issue_codes = [&](int kstep, uint4 (&w)[2][2], int half) {
         const int k = min(kstep, nk - 1);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
             w[nb][half] = *reinterpret_cast<const uint4 *>(qrow[nb] + (int64_t)k * kSpanBytes + half * 16);
     };
-    auto issue_scales = [&](int kstep, uint32_t (&s)[2]) {
-        const int k = min(kstep, nk - 1);
+    auto issue_window = [&](int kstep, uint2 (&w)[2]) {  // steps kstep .. kstep + 3 (clamped: nk % 4 == 0)
+        const int k = min(kstep, nk - 4);
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) s[nb] = srow[nb][k];
+        for (int nb = 0; nb < 2; ++nb) w[nb] = *reinterpret_cast<const uint2 *>(srow[nb] + k);
     };
     // the span sums of stage st's 64 rows (K step grp): 4 threads a row, 4 slots each (any slot order sums the row)
     auto sum_rows = [&](int st, int grp) __attribute__((always_inline)) {
@@ -246,8 +249,15 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         // value v is slot 8 (v / 4) + 4 h + v % 4 of its tile
         float s_[2];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) s_[nb] = bf16_to_f32(cs[RS][nb]);
-        issue_scales(k + 2, cs[RS]);
+        for (int nb = 0; nb < 2; ++nb) {
+            const uint32_t wd = (st & 2) ? wcur[nb].y : wcur[nb].x;
+            s_[nb] = __uint_as_float((st & 1) ? (wd & 0xFFFF0000u) : (wd << 16));
+        }
+        if (st == 3) {  // the next window becomes current (loaded four steps ago); the one after is issued
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) wcur[nb] = wnxt[nb];
+            issue_window(k + 5, wnxt);
+        }
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             if (tb == 1 && !TWO) continue;
@@ -275,8 +285,8 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     // prologue: steps 0..2 of activations, 0..1 of weights, and the sums of step 0
 #pragma unroll
     for (int s = 0; s < kStages - 1; ++s) issue_x(s, s);
-    issue_codes(0, cw[0], 0), issue_codes(0, cw[0], 1), issue_scales(0, cs[0]);
-    issue_codes(1, cw[1], 0), issue_codes(1, cw[1], 1), issue_scales(1, cs[1]);
+    issue_codes(0, cw[0], 0), issue_codes(0, cw[0], 1), issue_window(0, wcur);
+    issue_codes(1, cw[1], 0), issue_codes(1, cw[1], 1), issue_window(4, wnxt);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the first steps landed everywhere
     sum_rows(0, 0);
     // unrolled by the stage count (a multiple of the ring depth) so that stages and ring slots are constants; one
@@ -375,7 +385,7 @@ hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
 }  // namespace
 
 bool eligible(int bits, int64_t G, int64_t K, int act) {
-    return bits == 4 && G == 128 && K % kSpan == 0 && K >= kSpan && K <= kSpan * kMaxGroups && act == SX_ACT_BF16;
+    return bits == 4 && G == 128 && K % (4 * kSpan) == 0 && K <= kSpan * kMaxGroups && act == SX_ACT_BF16;
 }
 
 hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int32_t *ws, int64_t M, int64_t A,

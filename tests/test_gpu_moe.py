@@ -225,7 +225,7 @@ def test_grouped_matches_per_slot_oracle(M, A, E, I, d):
     assert err.cpu().numpy()[0] == 0
 
 
-@pytest.mark.parametrize("M,A,E,I,d", [(96, 4, 8, 256, 512), (40, 3, 5, 128, 256), (64, 2, 3, 384, 1024)])
+@pytest.mark.parametrize("M,A,E,I,d", [(96, 4, 8, 512, 512), (40, 3, 5, 512, 2048), (64, 2, 3, 1024, 1024)])
 def test_prefill_grouped_mfma_matches_oracle(M, A, E, I, d):
     """Prefill width (M >= 32 takes the 64-slot x 128-row MFMA kernel): gather, SwiGLU gather and combine against the
     oracle, with one bucket far over 64 slots (several wide tiles), one of exactly 64, and an invalid id (NaN rows,
