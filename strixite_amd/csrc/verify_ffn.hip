@@ -83,38 +83,43 @@ __device__ void build_units(Routes &R, uint32_t *emask, int S, int A, int Ew) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// gate_up + SwiGLU. LDS (static): the M activation rows [M][K + 8] BF16 in the B operand's code order, their span
-// sums [K / 128][16] and a zero block for the MFMA rows past M.
-template <int NV, int NB>
+// gate_up + SwiGLU. A block takes an equal run of the (expert, 16-feature tile) items (to within one item of every
+// other block); its 8 waves split K Q ways (Q = K / 512: four spans a wave) and take 8 / Q items a round, so every
+// wave of the grid streams the same bytes: 8 loads a round (4 spans x gate, up), 2 rounds in flight. The Q partial
+// tiles of an item are summed in LDS after a barrier (Q > 1), in K order, and the item's SwiGLU rows are stored by
+// the Q waves that made them, a quarter-tile or less each. A wave's four spans of the M activation rows sit in its
+// registers as MFMA A operands (code order) for the whole kernel, with their span sums. LDS (static): the partial
+// tiles of two rounds, the routing.
+template <int NV, int Q>
 __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[kXsElems];
-    __shared__ __attribute__((aligned(16))) float xsum[kMaxSpansGu * 16];
-    __shared__ __attribute__((aligned(16))) uint16_t zero_block[kZeroBytes / 2];
+    constexpr int P = kWaves / Q;  // items a round
+    __shared__ __attribute__((aligned(16))) float red[2][kWaves][2][4][64];  // [round & 1][wave][gate, up][v][lane]
     __shared__ Routes R;
     __shared__ uint32_t emask[kMaxExperts];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ip = wave / Q, kq = wave % Q;  // item lane, K slice (spans 4 kq .. 4 kq + 3)
     const int M = p.M, A = p.A, S = M * A, Ew = p.Ew;
-    const int64_t K = p.K, ldx = K + 8;
-    const int nspan = (int)(K / kSpan), chunks8 = (int)(K / 8), lg_chunks = __builtin_ctz((unsigned)chunks8);
-    const int n_items_x = M * chunks8;
+    const int64_t K = p.K;
+    const int n16 = lane & 15, g = lane >> 4;
 
-    // 1. this wave's logits (tokens wave and wave + 8, clamped: a redundant row past M), then the activations: the
-    // routing waits for its own loads only
+    // 1. this wave's logits (tokens wave and wave + 8, clamped: a redundant row past M), then its activations: A
+    // operand (span so, MFMA t) of lane (n16, g) = x[n16][128 (4 kq + so) + 32 g + 8 t ..+ 7] in code order
     const float *row0 = p.logits + (int64_t)min(wave, M - 1) * p.ld, *row1 = p.logits + (int64_t)min(wave + kWaves, M - 1) * p.ld;
     float v0[NV], v1[NV];
     routing::load_logits<NV>([&](int e) { return row0[e]; }, p.E, v0);
     routing::load_logits<NV>([&](int e) { return row1[e]; }, p.E, v1);
     const float sl0 = p.shared_logit ? p.shared_logit[(int64_t)min(wave, M - 1) * p.shared_ld] : 0.f;
     const float sl1 = p.shared_logit ? p.shared_logit[(int64_t)min(wave + kWaves, M - 1) * p.shared_ld] : 0.f;
-    uint4 raw[NB];
+    uint4 xr[4][4];
+    {
+        const uint16_t *xrow = p.x + (int64_t)min(n16, M - 1) * K + (int64_t)kq * 4 * kSpan + g * 32;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int i = min(b * kThreads + tid, n_items_x - 1);
-        raw[b] = *reinterpret_cast<const uint4 *>(p.x + (int64_t)(i >> lg_chunks) * K + (int64_t)(i & (chunks8 - 1)) * 8);
+        for (int so = 0; so < 4; ++so)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xr[so][t] = *reinterpret_cast<const uint4 *>(xrow + so * kSpan + t * 8);
     }
-    for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(zero_block)[i] = 0u;
 
     // 2. routing, a wave a token (moe_router.hpp:11-23); only block 0 reports errors and writes ids / coef out
     const bool lead = blockIdx.x == 0;
@@ -143,149 +148,161 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
         }
     }
 
-    // 3. this wave's items: [i0, i1) of U x T16 (expert-major), split evenly over every wave of the grid
+    // 3. this block's items [b0, b1) of U x T16 (expert-major), in rounds of P
     const int T16 = (int)((Nrows + 15) / 16);
-    const int64_t F = (int64_t)U * T16, W = (int64_t)gridDim.x * kWaves, gw = (int64_t)blockIdx.x * kWaves + wave;
-    const int i0 = (int)(gw * F / W), my = (int)((gw + 1) * F / W) - i0;
+    const int64_t F = (int64_t)U * T16;
+    const int b0 = (int)(blockIdx.x * F / gridDim.x), b1 = (int)((blockIdx.x + 1) * F / gridDim.x);
+    const int groups = (b1 - b0 + P - 1) / P;  // rounds (block-uniform)
+    if (groups <= 0) return;
 
-    // 4. weight ring: gate and up alternate, SPG = 4 spans (groups) a ring group, scale / min windows of 4 BF16
-    constexpr int NW = 2, SPG = kPrefetch / NW;
-    const int n16 = lane & 15, g = lane >> 4;
+    // 4. weight ring: round r = the slice kq of item b0 + r P + ip (clamped into the run: a clamped round loads a
+    // valid tile and stores nothing); gate and up alternate, scale / min windows of the 4 spans
+    constexpr int NW = 2;
     const int64_t up_q = Nrows * rowbytes, up_g = Nrows * ngroups;
-    const int groups = my * (nspan / SPG);
     uint4 ring[kRing][kPrefetch];
     uint2 sw_n[kRing][NW], mw_n[kRing][NW];
-    int ic = 0, ii = 0;
+    int ii = 0;
     const uint8_t *iq = p.q;
     const uint16_t *is_ = p.scale, *im = p.minv;
-    auto iplace = [&]() {  // item i0 + ii (clamped into the item range; F > 0 here)
-        const int item = (int)min((int64_t)(i0 + ii), F - 1);
+    auto iplace = [&]() {
+        const int item = min(b0 + ii * P + ip, b1 - 1);
         const int u = item / T16, tile = item - u * T16;
         const int64_t n = (int64_t)tile * 16 + n16, nn = n < Nrows ? n : Nrows - 1;
         const int64_t row = (int64_t)R.u_exp[u] * p.N + nn;
-        iq = p.q + row * rowbytes + g * 16;
-        is_ = p.scale + row * ngroups;
-        im = p.minv + row * ngroups;
+        iq = p.q + row * rowbytes + kq * 4 * kSpanBytes + g * 16;
+        is_ = p.scale + row * ngroups + kq * 4;
+        im = p.minv + row * ngroups + kq * 4;
     };
     auto advance_issue = [&]() {
-        if (ic + SPG < nspan) {
-            ic += SPG;
-            return;
-        }
-        ic = 0, ++ii;
+        ++ii;
         iplace();
     };
     auto issue_window = [&](uint2 (&sw)[NW], uint2 (&mw)[NW]) {
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            sw[w] = *reinterpret_cast<const uint2 *>(is_ + (w ? up_g : 0) + ic);
-            mw[w] = *reinterpret_cast<const uint2 *>(im + (w ? up_g : 0) + ic);
+            sw[w] = *reinterpret_cast<const uint2 *>(is_ + (w ? up_g : 0));
+            mw[w] = *reinterpret_cast<const uint2 *>(im + (w ? up_g : 0));
         }
     };
     auto issue_slot = [&](uint4 (&slot)[kPrefetch], int s) {
-        const int span = ic + s / NW, w = s % NW;
+        const int span = s / NW, w = s % NW;
         slot[s] = *reinterpret_cast<const uint4 *>(iq + (w ? up_q : 0) + (int64_t)span * kSpanBytes);
     };
-    if (U == 0) return;  // uniform: every slot invalid (handled above)
     __builtin_amdgcn_sched_barrier(0);
     iplace();
 #pragma unroll
     for (int r = 0; r < kRing; ++r) {
-        if (r > 0 && r < groups) advance_issue();
+        if (r > 0) advance_issue();  // unconditional (iplace clamps): a branch here would copy the ring behind a full wait
         issue_window(sw_n[r], mw_n[r]);
 #pragma unroll
         for (int s = 0; s < kPrefetch; ++s) issue_slot(ring[r], s);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 5. activations into LDS (q4 code order) with their span sums
+    // 5. the A operands (zero rows past M) and the span sums of the tokens of this lane's D rows 4 g + v
+    bf16x8 aop[4][4];
+    float xv[4][4];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int i = b * kThreads + tid;
-        if (i < n_items_x) {  // a span's 16 lanes are all in or all out (kThreads, chunks8 are multiples of 16)
-            const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
-            uint4 planes[1];
-            float sum;
-            qmm::detail::chunk_planes<4, 1, uint16_t>(raw[b], planes, sum);
-            *reinterpret_cast<uint4 *>(xs + r * ldx + (int64_t)c8 * 8) = planes[0];
-            sum = qmm::detail::group_sum_c<16>(sum);
-            if ((c8 & 15) == 0) xsum[(c8 >> 4) * 16 + r] = sum;
+    for (int so = 0; so < 4; ++so) {
+        float sum = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint4 raw = n16 < M ? xr[so][t] : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t d = qmm::detail::dword(raw, e);
+                sum += __uint_as_float(d << 16) + __uint_as_float(d & 0xFFFF0000u);
+            }
+            aop[so][t] = __builtin_bit_cast(bf16x8, uint4{__builtin_amdgcn_perm(raw.z, raw.x, 0x05040100u),
+                                                          __builtin_amdgcn_perm(raw.z, raw.x, 0x07060302u),
+                                                          __builtin_amdgcn_perm(raw.w, raw.y, 0x05040100u),
+                                                          __builtin_amdgcn_perm(raw.w, raw.y, 0x07060302u)});
         }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xv[so][v] = __shfl(sum, 4 * g + v);
     }
-    for (int i = tid; i < nspan * 16; i += kThreads)
-        if ((i & 15) >= M) xsum[i] = 0.f;
-    __syncthreads();
-    if (my <= 0) return;
+
+    // the D rows 4 g + vb .. 4 g + vb + VS - 1 whose SwiGLU this wave stores (Q = 8: on half the lanes)
+    constexpr int VS = Q >= 4 ? 1 : 4 / Q;
+    const int vb = Q == 8 ? kq >> 1 : kq * VS;
+    const bool st_lane = Q != 8 || (g & 1) == (kq & 1);
+    auto epilogue = [&](int item, const float (&gate)[VS], const float (&up)[VS]) __attribute__((always_inline)) {
+        const int u = item / T16, tile = item - u * T16;
+        const uint32_t mask = R.u_mask[u];
+        const int64_t n = (int64_t)tile * 16 + n16;
+        if (n >= Nrows || !st_lane) return;
+#pragma unroll
+        for (int j = 0; j < VS; ++j) {
+            const int r = 4 * g + vb + j;
+            if (r >= M || !((mask >> r) & 1u)) continue;
+            const float gv = as_bf16(gate[j]), uv = as_bf16(up[j]);
+            const float hv = as_bf16(silu(gv)) * uv;
+            p.h[(int64_t)R.slot_tab[u][r] * Nrows + n] = (uint16_t)f32_to_bf16(hv);
+        }
+    };
 
     // 6. consume: A rows = tokens (lane row n16), D rows 4g .. 4g + 3 = tokens, columns = the 16 features
-    const bool a_on = n16 < M;
-    const uint16_t *a_row = a_on ? xs + n16 * ldx + g * 32 : zero_block;
-    const int64_t a_step = a_on ? kSpan : 0;  // the zero block is re-read for every span
-    int cc = 0, ci = 0;
-    f32x4 acc[NW];
-#pragma unroll
-    for (int w = 0; w < NW; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto consume = [&](int gr, auto slot_tag) {
+    auto consume = [&](int gr, auto slot_tag) __attribute__((always_inline)) {
         constexpr int RS = decltype(slot_tag)::value;
         uint2 sw[NW], mw[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) sw[w] = sw_n[RS][w], mw[w] = mw_n[RS][w];
         if (gr + kRing < groups) advance_issue();
         issue_window(sw_n[RS], mw_n[RS]);
-        const uint16_t *ab = a_row + cc * a_step;
-        const float *xsg = xsum + cc * 16 + 4 * g;
+        float acc[NW][4] = {};
 #pragma unroll
         for (int s = 0; s < kPrefetch; ++s) {
             const int w = s % NW, so = s / NW;
-            const uint4 w_cur = ring[RS][s];
+            bf16x8 bop[4];  // unpacked before the reload is issued: the slot's register is then free for it (a
+                            // value still live there would make the loop rotate the ring behind a full wait)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) bop[t] = qmm::detail::codes_b<4>(ring[RS][s], t);
             issue_slot(ring[RS], s);
             f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8 *>(ab + so * a_step + t * 8);
-                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, qmm::detail::codes_b<4>(w_cur, t), D, 0, 0, 0);
-            }
-            const float4 xv = *reinterpret_cast<const float4 *>(xsg + so * 16);
+            for (int t = 0; t < 4; ++t) D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[so][t], bop[t], D, 0, 0, 0);
             const uint32_t swd = so < 2 ? sw[w].x : sw[w].y, mwd = so < 2 ? mw[w].x : mw[w].y;
             const float s_ = __uint_as_float((so & 1) ? (swd & 0xFFFF0000u) : (swd << 16));
             const float m_ = __uint_as_float((so & 1) ? (mwd & 0xFFFF0000u) : (mwd << 16));
             const float cm = fmaf(-128.f, s_, m_);
-            acc[w][0] = fmaf(s_, D[0], fmaf(cm, xv.x, acc[w][0]));
-            acc[w][1] = fmaf(s_, D[1], fmaf(cm, xv.y, acc[w][1]));
-            acc[w][2] = fmaf(s_, D[2], fmaf(cm, xv.z, acc[w][2]));
-            acc[w][3] = fmaf(s_, D[3], fmaf(cm, xv.w, acc[w][3]));
-        }
-        if (gr >= groups) return;  // the phantom group
-        if (cc + SPG < nspan) {
-            cc += SPG;
-            return;
-        }
-        cc = 0;
-        const int item = i0 + ci;
-        const int u = item / T16, tile = item - u * T16;
-        const uint32_t mask = R.u_mask[u];
-        const int64_t n = (int64_t)tile * 16 + n16;
-        if (n < Nrows) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int r = 4 * g + v;
-                if (r >= M || !((mask >> r) & 1u)) continue;
-                const float gv = as_bf16(acc[0][v]), uv = as_bf16(acc[1][v]);
-                const float hv = as_bf16(silu(gv)) * uv;
-                p.h[(int64_t)R.slot_tab[u][r] * Nrows + n] = (uint16_t)f32_to_bf16(hv);
+            for (int v = 0; v < 4; ++v) acc[w][v] = fmaf(s_, D[v], fmaf(cm, xv[so][v], acc[w][v]));
+        }
+        if (gr >= groups) return;  // the phantom round
+        const int item = b0 + gr * P + ip;
+        if constexpr (Q == 1) {
+            if (item < b1) epilogue(item, acc[0], acc[1]);
+        } else {
+            float(&mine)[2][4][64] = red[gr & 1][wave];
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) mine[w][v][lane] = acc[w][v];
+            // every wave's partial tile of this round is in LDS (the loads in flight stay in flight); the next
+            // write to this half of red comes after the next round's barrier, when these reads are done
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (item < b1) {
+                float gate[VS] = {}, up[VS] = {};
+#pragma unroll
+                for (int qq = 0; qq < Q; ++qq) {  // K order
+                    const float(&part)[2][4][64] = red[gr & 1][ip * Q + qq];
+#pragma unroll
+                    for (int j = 0; j < VS; ++j) gate[j] += part[0][vb + j][lane], up[j] += part[1][vb + j][lane];
+                }
+                epilogue(item, gate, up);
             }
         }
-#pragma unroll
-        for (int w = 0; w < NW; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
-        ++ci;
     };
-    // Runs of kRing groups, all issuing their loads (a count short of a multiple of kRing ends with phantom groups
-    // that re-load the last one and stop after their MFMAs): a consume whose loads were conditional would merge two
-    // versions of the ring registers, and the copies at such a merge wait for every outstanding load.
+    // Runs of kRing rounds, all issuing their loads (an odd count ends with a phantom round that re-loads the last
+    // one and stops after its MFMAs): a consume whose loads were conditional would merge two versions of the ring
+    // registers, and the copies at such a merge wait for every outstanding load.
     for (int gr = 0; gr < groups; gr += kRing) {
         consume(gr, std::integral_constant<int, 0>{});
         consume(gr + 1, std::integral_constant<int, 1>{});
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave exits
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -366,7 +383,7 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     iplace();
 #pragma unroll
     for (int r = 0; r < kRing; ++r) {
-        if (r > 0 && r < groups) advance_issue();
+        if (r > 0) advance_issue();  // unconditional (iplace clamps): a branch here would copy the ring behind a full wait
         issue_window(sw_n[r], mw_n[r]);
 #pragma unroll
         for (int s = 0; s < kPrefetch; ++s) issue_slot(ring[r], s);
@@ -414,13 +431,15 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
         const uint16_t *ab = a_row + cc * a_step;
 #pragma unroll
         for (int s = 0; s < kPrefetch; ++s) {
-            const uint4 w_cur = ring[RS][s];
+            bf16x8 bop[4];  // unpacked before the reload is issued: the slot's register is then free for it
+#pragma unroll
+            for (int t = 0; t < 4; ++t) bop[t] = qmm::detail::codes_b<4>(ring[RS][s], t);
             issue_slot(ring[RS], s);
             f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const bf16x8 av = *reinterpret_cast<const bf16x8 *>(ab + s * a_step + t * 8);
-                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, qmm::detail::codes_b<4>(w_cur, t), D, 0, 0, 0);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bop[t], D, 0, 0, 0);
             }
             const uint32_t swd = qmm::detail::dword(sw, s >> 1), mwd = qmm::detail::dword(mw, s >> 1);
             const float s_ = __uint_as_float((s & 1) ? (swd & 0xFFFF0000u) : (swd << 16));
@@ -475,21 +494,21 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
 }  // namespace
 
 hipError_t launch_gate_up(const GateUpParams &p, int cus, hipStream_t stream) {
-    const int n_items = p.M * (int)(p.K / 8);
-    const int nb = (n_items + kThreads - 1) / kThreads;
     const int nv = p.E <= 256 ? 4 : p.E <= 512 ? 8 : 16;
+    const int q = (int)(p.K / 512);  // K in {512, 1024, 2048, 4096}: four spans a wave
     const dim3 grid((unsigned)cus);
-    auto go = [&](auto nv_tag, auto nb_tag) {
-        gate_up_kernel<decltype(nv_tag)::value, decltype(nb_tag)::value><<<grid, kThreads, 0, stream>>>(p);
+    auto go = [&](auto nv_tag, auto q_tag) {
+        gate_up_kernel<decltype(nv_tag)::value, decltype(q_tag)::value><<<grid, kThreads, 0, stream>>>(p);
     };
-    auto by_nb = [&](auto nv_tag) {
-        if (nb <= 4) go(nv_tag, std::integral_constant<int, 4>{});
-        else if (nb <= 8) go(nv_tag, std::integral_constant<int, 8>{});
-        else go(nv_tag, std::integral_constant<int, 16>{});
+    auto by_q = [&](auto nv_tag) {
+        if (q == 1) go(nv_tag, std::integral_constant<int, 1>{});
+        else if (q == 2) go(nv_tag, std::integral_constant<int, 2>{});
+        else if (q == 4) go(nv_tag, std::integral_constant<int, 4>{});
+        else go(nv_tag, std::integral_constant<int, 8>{});
     };
-    if (nv == 4) by_nb(std::integral_constant<int, 4>{});
-    else if (nv == 8) by_nb(std::integral_constant<int, 8>{});
-    else by_nb(std::integral_constant<int, 16>{});
+    if (nv == 4) by_q(std::integral_constant<int, 4>{});
+    else if (nv == 8) by_q(std::integral_constant<int, 8>{});
+    else by_q(std::integral_constant<int, 16>{});
     return hipGetLastError();
 }
 
@@ -519,8 +538,7 @@ int check_gate_up(const char *fn, int64_t M, int64_t A, int64_t E, int64_t k, in
     SX_CHECK(w->G == 128 && w->N % Ew == 0 && (w->N / Ew) % 2 == 0, fn, " gate_up view N = ", w->N, ", G = ", w->G,
              ": needs G = 128 and N a multiple of 2 Ew");
     const int64_t K = w->K;
-    SX_CHECK((K == 512 || K == 1024 || K == 2048 || K == 4096) && M * (K + 8) <= vf::kXsElems, fn, " K = ", K,
-             " with M = ", M, " does not fit the fused kernel");
+    SX_CHECK(K == 512 || K == 1024 || K == 2048 || K == 4096, fn, " K = ", K, " does not fit the fused kernel");
     SX_CHECK(aligned(w->scale, 8) && aligned(w->minv, 8) && aligned(w->q, 16), fn, " weight arrays misaligned");
     return SX_OK;
 }

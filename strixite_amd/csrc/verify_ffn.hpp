@@ -8,7 +8,6 @@ constexpr int kMaxSlots = 64;        // M * A
 constexpr int kMaxTokens = 16;       // M: the rows of one MFMA tile
 constexpr int kMaxExperts = 1024;    // experts in the weights
 constexpr int kMaxSpansGu = 32;      // gate_up K <= 4096
-constexpr int kXsElems = 16 * 4104;  // gate_up: M * (K + 8) BF16 activations in LDS
 constexpr int kMaxSpansDn = 16;      // down K <= 2048
 constexpr int kHsElems = 64 * 1032;  // down: M * A * (K + 8) BF16 rows of h in LDS
 
