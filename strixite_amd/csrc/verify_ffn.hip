@@ -33,6 +33,7 @@ using qmm::detail::kPrefetch;
 constexpr int kThreads = 512, kWaves = 8;
 constexpr int kRing = 2;  // groups of 8 loads in flight a wave (16 KB a wave, 128 KB a CU; 3 measured slower)
 constexpr int kSpan = 128, kSpanBytes = 64;
+constexpr int kSpansDn = 4, kRingDn = 4;  // down: an item is 4 spans of a unit (4 loads a wave), 4 items in flight
 constexpr int kZeroBytes = qmm::detail::kZeroBytes;
 
 struct Routes {                // one block's copy of the routing (LDS)
@@ -348,45 +349,43 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
 
     const int64_t rowbytes = K / 2, ngroups = K / kSpan;
     const int n16 = lane & 15, g = lane >> 4;
-    const int my = U > wave ? (U - wave + kWaves - 1) / kWaves : 0;  // units wave, wave + 8, ...
-    constexpr int SPG = kPrefetch;
-    const int groups = my * (nspan / SPG);
-    uint4 ring[kRing][kPrefetch];
-    uint4 sw_n[kRing], mw_n[kRing];
-    int ic = 0, ii = 0;
+    // items: (unit, chunk of 4 spans), unit-major; this wave's share [i0, i0 + groups), equal to within one item
+    constexpr int SPG = kSpansDn;
+    const int C = nspan / SPG, F = U * C;
+    const int i0 = wave * F / kWaves, groups = (wave + 1) * F / kWaves - i0;
+    uint4 ring[kRingDn][SPG];
+    uint2 sw_n[kRingDn], mw_n[kRingDn];
+    int ii = 0;
     const uint8_t *iq = p.q;
     const uint16_t *is_ = p.scale, *im = p.minv;
-    auto iplace = [&]() {
-        const int u = min(wave + ii * kWaves, U - 1);  // past the units (or none): a valid row, never used
+    auto iplace = [&]() {  // item i0 + ii, clamped into the items (or the first row when there are none)
+        const int item = max(min(i0 + ii, F - 1), 0);
+        const int u = item / C, c = item - u * C;
         const int64_t n = n0 + n16, nn = n < N ? n : N - 1;
-        const int64_t row = (int64_t)(u >= 0 ? R.u_exp[u] : 0) * N + nn;
-        iq = p.q + row * rowbytes + g * 16;
-        is_ = p.scale + row * ngroups;
-        im = p.minv + row * ngroups;
+        const int64_t row = (int64_t)(F > 0 ? R.u_exp[u] : 0) * N + nn;
+        iq = p.q + row * rowbytes + c * SPG * kSpanBytes + g * 16;
+        is_ = p.scale + row * ngroups + c * SPG;
+        im = p.minv + row * ngroups + c * SPG;
     };
     auto advance_issue = [&]() {
-        if (ic + SPG < nspan) {
-            ic += SPG;
-            return;
-        }
-        ic = 0, ++ii;
+        ++ii;
         iplace();
     };
-    auto issue_window = [&](uint4 &sw, uint4 &mw) {
-        sw = *reinterpret_cast<const uint4 *>(is_ + ic);
-        mw = *reinterpret_cast<const uint4 *>(im + ic);
+    auto issue_window = [&](uint2 &sw, uint2 &mw) {
+        sw = *reinterpret_cast<const uint2 *>(is_);
+        mw = *reinterpret_cast<const uint2 *>(im);
     };
-    auto issue_slot = [&](uint4 (&slot)[kPrefetch], int s) {
-        slot[s] = *reinterpret_cast<const uint4 *>(iq + (int64_t)(ic + s) * kSpanBytes);
+    auto issue_slot = [&](uint4 (&slot)[SPG], int s) {
+        slot[s] = *reinterpret_cast<const uint4 *>(iq + (int64_t)s * kSpanBytes);
     };
     __builtin_amdgcn_sched_barrier(0);
     iplace();
 #pragma unroll
-    for (int r = 0; r < kRing; ++r) {
+    for (int r = 0; r < kRingDn; ++r) {
         if (r > 0) advance_issue();  // unconditional (iplace clamps): a branch here would copy the ring behind a full wait
         issue_window(sw_n[r], mw_n[r]);
 #pragma unroll
-        for (int s = 0; s < kPrefetch; ++s) issue_slot(ring[r], s);
+        for (int s = 0; s < SPG; ++s) issue_slot(ring[r], s);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -405,33 +404,26 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     }
     __syncthreads();
 
-    // consume: per unit, A row n16 = token n16's slot of the expert (or zeros); D rows 4g + v = tokens
+    // consume: per item, A row n16 = token n16's slot of the unit's expert (or zeros); D rows 4g + v = tokens
     float yacc[4] = {0.f, 0.f, 0.f, 0.f};
-    int cc = 0, ci = 0;
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint16_t *a_row = zero_block;
-    int64_t a_step = 0;
-    int sv[4] = {-1, -1, -1, -1};  // the slots of D rows 4g + v under the current unit
-    auto unit_begin = [&]() {
-        const int u = wave + ci * kWaves;
-        const int sa = R.slot_tab[u][n16];
-        a_row = sa >= 0 ? hs + sa * ldh + g * 32 : zero_block;
-        a_step = sa >= 0 ? kSpan : 0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            sv[v] = R.slot_tab[u][4 * g + v];
-        }
-    };
-    if (groups > 0) unit_begin();
-    auto consume = [&](int gr, auto slot_tag) {
+    auto consume = [&](int gr, auto slot_tag) __attribute__((always_inline)) {
         constexpr int RS = decltype(slot_tag)::value;
-        const uint4 sw = sw_n[RS], mw = mw_n[RS];
-        if (gr + kRing < groups) advance_issue();
+        const uint2 sw = sw_n[RS], mw = mw_n[RS];
+        if (gr + kRingDn < groups) advance_issue();
         issue_window(sw_n[RS], mw_n[RS]);
-        const uint16_t *ab = a_row + cc * a_step;
+        const int item = max(min(i0 + gr, F - 1), 0);
+        const int u = item / C, c0 = (item - u * C) * SPG;
+        const int sa = R.slot_tab[u][n16];
+        const uint16_t *ab = sa >= 0 ? hs + sa * ldh + g * 32 + c0 * kSpan : zero_block;
+        const int a_step = sa >= 0 ? kSpan : 0;
+        int sv[4];
 #pragma unroll
-        for (int s = 0; s < kPrefetch; ++s) {
-            bf16x8 bop[4];  // unpacked before the reload is issued: the slot's register is then free for it
+        for (int v = 0; v < 4; ++v) sv[v] = R.slot_tab[u][4 * g + v];
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < SPG; ++s) {
+            bf16x8 bop[4];  // unpacked before the reload is issued: the slot's register is then free for it (a
+                            // value still live there would make the loop rotate the ring behind a full wait)
 #pragma unroll
             for (int t = 0; t < 4; ++t) bop[t] = qmm::detail::codes_b<4>(ring[RS][s], t);
             issue_slot(ring[RS], s);
@@ -441,35 +433,31 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
                 const bf16x8 av = *reinterpret_cast<const bf16x8 *>(ab + s * a_step + t * 8);
                 D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bop[t], D, 0, 0, 0);
             }
-            const uint32_t swd = qmm::detail::dword(sw, s >> 1), mwd = qmm::detail::dword(mw, s >> 1);
+            const uint32_t swd = s < 2 ? sw.x : sw.y, mwd = s < 2 ? mw.x : mw.y;
             const float s_ = __uint_as_float((s & 1) ? (swd & 0xFFFF0000u) : (swd << 16));
             const float m_ = __uint_as_float((s & 1) ? (mwd & 0xFFFF0000u) : (mwd << 16));
             const float cm = fmaf(-128.f, s_, m_);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float xv = sv[v] >= 0 ? hsum[sv[v] * nspan + cc + s] : 0.f;
+                const float xv = sv[v] >= 0 ? hsum[sv[v] * nspan + c0 + s] : 0.f;
                 acc[v] = fmaf(s_, D[v], fmaf(cm, xv, acc[v]));
             }
         }
-        if (gr >= groups) return;  // the phantom group
-        if (cc + SPG < nspan) {
-            cc += SPG;
-            return;
-        }
-        cc = 0;
+        if (gr >= groups) return;  // a phantom item
 #pragma unroll
         for (int v = 0; v < 4; ++v)
             if (sv[v] >= 0) yacc[v] = fmaf(R.coef[sv[v]], acc[v], yacc[v]);
-        acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (++ci < my) unit_begin();
     };
-    // Runs of kRing groups, all issuing their loads (a count short of a multiple of kRing ends with phantom groups
-    // that re-load the last one and stop after their MFMAs): a consume whose loads were conditional would merge two
+    // Runs of kRingDn items, all issuing their loads (a count short of a multiple ends with phantom items that
+    // re-load the last one and stop after their MFMAs): a consume whose loads were conditional would merge two
     // versions of the ring registers, and the copies at such a merge wait for every outstanding load.
-    for (int gr = 0; gr < groups; gr += kRing) {
+    for (int gr = 0; gr < groups; gr += kRingDn) {
         consume(gr, std::integral_constant<int, 0>{});
         consume(gr + 1, std::integral_constant<int, 1>{});
+        consume(gr + 2, std::integral_constant<int, 2>{});
+        consume(gr + 3, std::integral_constant<int, 3>{});
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom items' loads land before the wave exits
 
     // the waves' sums in wave order; tokens with an invalid slot get NaN rows (the combine's rule)
 #pragma unroll
