@@ -10,12 +10,12 @@ from . import kernels as kx
 
 class MoeVerifyLayer:
     """One MoE FFN sublayer. Weights: Wr FP32 [E, d], gate_up q4 [E * 2I, d], down q4 [E * d, I] (experts stacked,
-    runtime/qwen4exp.cpp:126-129). At verify width (the shapes kernels.verify_supported takes) three launches: router
-    projection -> routing + gate_up + SwiGLU -> down + combine (single_launch=True: the last two as one cooperative
-    launch), the sequence qwen4exp.cpp:1139-1163 runs below kGroupedMinTokens. Otherwise (or fused=False): router projection -> moe_router + moe_group_routes -> grouped
+    runtime/qwen4exp.cpp:126-129). At verify width (the shapes kernels.verify_supported takes) two launches: router
+    projection -> routing + gate_up + SwiGLU + down + combine in one cooperative launch (single_launch=False: the last
+    as two launches), the sequence qwen4exp.cpp:1139-1163 runs below kGroupedMinTokens. Otherwise (or fused=False): router projection -> moe_router + moe_group_routes -> grouped
     gate_up with the SwiGLU epilogue -> grouped down + combine."""
 
-    def __init__(self, Wr, gate_up, down, E, k, max_tokens, act_dtype=torch.bfloat16, fused=True, single_launch=False):
+    def __init__(self, Wr, gate_up, down, E, k, max_tokens, act_dtype=torch.bfloat16, fused=True, single_launch=True):
         self.Wr, self.gate_up, self.down, self.E, self.k = Wr, gate_up, down, E, k
         self.d = gate_up.K
         self.I = down.K
