@@ -110,15 +110,6 @@ int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t
 /* y [M, N] = sum_a coef[m, a] * (h[m, a] W_down[ids[m, a]]^T); NaN rows for tokens with an invalid slot. */
 int sx_moe_verify_down(const void *h, int64_t M, int64_t A, const int32_t *ids, const float *coef,
                        const sx_qview *down, int64_t Ew, void *y, int act, uint32_t *expert_err, sx_stream stream);
-/* sx_moe_verify_gate_up then sx_moe_verify_down in one cooperative launch (one block a CU, all resident): the same
- * ids, coef, h and y. sync: a device uint64 the launch's grid barrier counts arrivals on; zero it once, then reuse
- * it for every call on one stream (concurrent calls need their own). If the barrier wait ever exceeds 0.2 s the
- * kernel gives up instead of hanging: expert_err = {1, 0xFFFFFFFE, block} and y is not written (zero sync again
- * before the next call). Replaces the runtime/qwen4exp.cpp:1139-1163 sequence below kGroupedMinTokens. */
-int sx_moe_verify_ffn(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
-                      const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *gate_up,
-                      const sx_qview *down, int64_t Ew, int32_t *ids, float *coef, void *h, void *y, int act,
-                      uint32_t *router_err, uint32_t *expert_err, uint64_t *sync, sx_stream stream);
 /* y [M, A, N] (linear_q4_experts_gather_grouped, moe_grouped.hpp:53-55). */
 int sx_linear_q4_experts_gather_grouped(const void *x, const sx_qview *w, int64_t E, const void *ws, size_t ws_bytes,
                                         int64_t M, int64_t A, void *y, int act, int math, sx_stream stream);

@@ -91,14 +91,12 @@ __device__ void build_units(Routes &R, uint32_t *emask, int S, int A, int Ew) {
 // the Q waves that made them, a quarter-tile or less each. A wave's four spans of the M activation rows sit in its
 // registers as MFMA A operands (code order) for the whole kernel, with their span sums. LDS (static): the partial
 // tiles of two rounds, the routing.
-struct GateUpLds {
-    float red[2][kWaves][2][4][64];  // [round & 1][wave][gate, up][v][lane]: the partial tiles
-};
-
 template <int NV, int Q>
-__device__ __forceinline__ void gate_up_body(const GateUpParams &p, Routes &R, uint32_t *emask, GateUpLds &L) {
+__global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
     constexpr int P = kWaves / Q;  // items a round
-    auto &red = L.red;
+    __shared__ __attribute__((aligned(16))) float red[2][kWaves][2][4][64];  // [round & 1][wave][gate, up][v][lane]
+    __shared__ Routes R;
+    __shared__ uint32_t emask[kMaxExperts];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -305,37 +303,20 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, Routes &R, u
         consume(gr, std::integral_constant<int, 0>{});
         consume(gr + 1, std::integral_constant<int, 1>{});
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave goes on
-}
-
-template <int NV, int Q>
-__global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
-    __shared__ __attribute__((aligned(16))) GateUpLds L;
-    __shared__ Routes R;
-    __shared__ uint32_t emask[kMaxExperts];
-    gate_up_body<NV, Q>(p, R, emask, L);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave exits
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 // down + combine. LDS (static): the S slot rows of h [S][K + 8] BF16 (code order), span sums [S][K / 128], a zero
 // block, the waves' partial sums [8][16 tokens][16 rows].
-struct DownLds {
-    uint16_t hs[kHsElems];                    // the slot rows of h, code order
-    float hsum[kMaxSlots * kMaxSpansDn];      // their span sums
-    uint16_t zero_block[kZeroBytes / 2];      // A operand rows of tokens without a slot
-    float red[kWaves][16][16];                // the waves' sums
-};
-
-// One 16-row block of the output (rows n0 ..). ROUTE: the block reads ids / coef and builds the units itself (the
-// standalone kernel); otherwise R holds them already. stage_h: load h into LDS (once per block: later row blocks
-// reuse it). between(): called once the first weight loads are in flight and before h is read; false skips the
-// rest (the fused kernel's grid barrier, which can time out).
-template <int NB, bool ROUTE, typename Between>
-__device__ __forceinline__ void down_body(const DownParams &p, Routes &R, uint32_t *emask, DownLds &L, int64_t n0,
-                                          bool stage_h, Between &&between) {
-    uint16_t *hs = L.hs, *zero_block = L.zero_block;
-    float *hsum = L.hsum;
-    auto &red = L.red;
+template <int NB>
+__global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t hs[kHsElems];
+    __shared__ __attribute__((aligned(16))) float hsum[kMaxSlots * kMaxSpansDn];
+    __shared__ __attribute__((aligned(16))) uint16_t zero_block[kZeroBytes / 2];
+    __shared__ __attribute__((aligned(16))) float red[kWaves][16][16];
+    __shared__ Routes R;
+    __shared__ uint32_t emask[kMaxExperts];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -343,31 +324,25 @@ __device__ __forceinline__ void down_body(const DownParams &p, Routes &R, uint32
     const int64_t K = p.K, ldh = K + 8, N = p.N;
     const int nspan = (int)(K / kSpan), chunks8 = (int)(K / 8), lg_chunks = __builtin_ctz((unsigned)chunks8);
     const int n_items_x = S * chunks8;
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
 
-    // standalone: the routing first, then the rows of h (the grouping waits for the ids only)
+    // the routing first, then the rows of h: the grouping waits for the ids only
+    int32_t my_id;
+    float my_coef;
+    my_id = p.ids[min(lane, S - 1)], my_coef = p.coef[min(lane, S - 1)];  // every wave: no branch around loads
     uint4 raw[NB];
-    auto load_h = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int i = min(b * kThreads + tid, n_items_x - 1);
-            raw[b] = *reinterpret_cast<const uint4 *>(p.h + (int64_t)(i >> lg_chunks) * K + (int64_t)(i & (chunks8 - 1)) * 8);
-        }
-    };
-    if constexpr (ROUTE) {
-        const int32_t my_id = p.ids[min(lane, S - 1)];  // every wave: no branch around loads
-        const float my_coef = p.coef[min(lane, S - 1)];
-        load_h();
-        R.ids[lane] = my_id, R.coef[lane] = my_coef;  // every wave the same values (unconditional: nothing sinks the loads)
+    for (int b = 0; b < NB; ++b) {
+        const int i = min(b * kThreads + tid, n_items_x - 1);
+        raw[b] = *reinterpret_cast<const uint4 *>(p.h + (int64_t)(i >> lg_chunks) * K + (int64_t)(i & (chunks8 - 1)) * 8);
     }
-    if (stage_h)
-        for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(zero_block)[i] = 0u;
-    if constexpr (ROUTE) {
-        __syncthreads();
-        build_units(R, emask, S, A, Ew);
-    }
+    R.ids[lane] = my_id, R.coef[lane] = my_coef;  // every wave the same values (unconditional: nothing sinks the loads)
+    for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(zero_block)[i] = 0u;
+    __syncthreads();
+    build_units(R, emask, S, A, Ew);
     const int U = __builtin_amdgcn_readfirstlane(R.U);
     const uint64_t bad_slots = R.bad_slots;
-    if (ROUTE && blockIdx.x == 0 && bad_slots && tid == 0) {
+    if (blockIdx.x == 0 && bad_slots && tid == 0) {
         const int s = __builtin_ctzll(bad_slots);
         flag_error(p.expert_err, (uint32_t)R.ids[s], (uint32_t)s);
     }
@@ -413,13 +388,11 @@ __device__ __forceinline__ void down_body(const DownParams &p, Routes &R, uint32
         for (int s = 0; s < SPG; ++s) issue_slot(ring[r], s);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (!between()) return;
-    if (!ROUTE && stage_h) load_h();
 
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int i = b * kThreads + tid;
-        if (stage_h && i < n_items_x) {
+        if (i < n_items_x) {
             const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
             uint4 planes[1];
             float sum;
@@ -506,74 +479,6 @@ __device__ __forceinline__ void down_body(const DownParams &p, Routes &R, uint32
     }
 }
 
-template <int NB>
-__global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
-    __shared__ __attribute__((aligned(16))) DownLds L;
-    __shared__ Routes R;
-    __shared__ uint32_t emask[kMaxExperts];
-    down_body<NB, true>(p, R, emask, L, (int64_t)blockIdx.x * 16, true, [] { return true; });
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// Both phases in one cooperative launch (every block resident at once): gate_up, a grid barrier, down. A block
-// arrives at the barrier as soon as its h rows are stored, issues its first down weight loads and only then waits,
-// so the down stream starts while the last gate_up blocks finish; the routing built for gate_up serves down as is.
-// The barrier counts arrivals on a 64-bit word that only grows (a launch's blocks wait for the next multiple of the
-// grid size), so it needs no reset between launches on one stream; a wait gives up after kSyncTimeoutTicks and
-// reports it instead of hanging.
-constexpr uint64_t kSyncTimeoutTicks = 20000000;  // 0.2 s of the 100 MHz s_memrealtime clock
-constexpr uint32_t kSyncTimeoutCode = 0xFFFFFFFEu;  // expert_err word 1 when the barrier timed out
-
-template <int NV, int Q, int NB>
-__global__ void __launch_bounds__(kThreads) ffn_kernel(GateUpParams gp, DownParams dp, uint64_t *sync) {
-    static_assert(sizeof(GateUpLds) <= sizeof(DownLds), "the gate_up LDS must fit the down LDS it shares");
-    __shared__ __attribute__((aligned(16))) unsigned char pool[sizeof(DownLds)];
-    __shared__ Routes R;
-    __shared__ uint32_t emask[kMaxExperts];
-    __shared__ uint64_t s_target;
-    __shared__ int s_ok;
-
-    gate_up_body<NV, Q>(gp, R, emask, *reinterpret_cast<GateUpLds *>(pool));
-
-    // arrive: this block's h stores are complete (every wave waits for its own), then made visible device-wide
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const uint64_t old = __hip_atomic_fetch_add(sync, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_target = (old / gridDim.x + 1) * gridDim.x;
-    }
-
-    bool waited = false, ok = true;
-    auto wait = [&]() -> bool {  // after the first row block's weight loads are issued
-        if (waited) return ok;
-        waited = true;
-        if (threadIdx.x == 0) {
-            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-            int good = 1;
-            while ((int64_t)(__hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - s_target) < 0) {
-                __builtin_amdgcn_s_sleep(2);
-                if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeoutTicks) {
-                    good = 0;
-                    break;
-                }
-            }
-            if (!good) flag_error(dp.expert_err, kSyncTimeoutCode, (uint32_t)blockIdx.x);
-            s_ok = good;
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // every other block's h stores are visible from here
-        ok = __builtin_amdgcn_readfirstlane(s_ok) != 0;
-        return ok;
-    };
-    const int nrb = (int)((dp.N + 15) / 16);
-    bool first = true;
-    for (int rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
-        down_body<NB, false>(dp, R, emask, *reinterpret_cast<DownLds *>(pool), (int64_t)rb * 16, first, wait);
-        first = false;
-        if (!ok) break;
-    }
-}
-
 }  // namespace
 
 hipError_t launch_gate_up(const GateUpParams &p, int cus, hipStream_t stream) {
@@ -603,34 +508,6 @@ hipError_t launch_down(const DownParams &p, hipStream_t stream) {
     else if (nb <= 8) down_kernel<8><<<grid, kThreads, 0, stream>>>(p);
     else down_kernel<16><<<grid, kThreads, 0, stream>>>(p);
     return hipGetLastError();
-}
-
-hipError_t launch_ffn(const GateUpParams &gp, const DownParams &dp, uint64_t *sync, int cus, hipStream_t stream) {
-    const int nv = gp.E <= 256 ? 4 : gp.E <= 512 ? 8 : 16;
-    const int q = (int)(gp.K / 512);
-    const int n_items = dp.M * dp.A * (int)(dp.K / 8);
-    const int nb = (n_items + kThreads - 1) / kThreads;
-    GateUpParams a = gp;
-    DownParams b = dp;
-    uint64_t *c = sync;
-    void *args[] = {&a, &b, &c};
-    const void *fn = nullptr;
-    auto pick = [&](auto nv_tag, auto q_tag) {
-        constexpr int NV = decltype(nv_tag)::value, Q = decltype(q_tag)::value;
-        if (nb <= 4) fn = reinterpret_cast<const void *>(&ffn_kernel<NV, Q, 4>);
-        else if (nb <= 8) fn = reinterpret_cast<const void *>(&ffn_kernel<NV, Q, 8>);
-        else fn = reinterpret_cast<const void *>(&ffn_kernel<NV, Q, 16>);
-    };
-    auto by_q = [&](auto nv_tag) {
-        if (q == 1) pick(nv_tag, std::integral_constant<int, 1>{});
-        else if (q == 2) pick(nv_tag, std::integral_constant<int, 2>{});
-        else if (q == 4) pick(nv_tag, std::integral_constant<int, 4>{});
-        else pick(nv_tag, std::integral_constant<int, 8>{});
-    };
-    if (nv == 4) by_q(std::integral_constant<int, 4>{});
-    else if (nv == 8) by_q(std::integral_constant<int, 8>{});
-    else by_q(std::integral_constant<int, 16>{});
-    return hipLaunchCooperativeKernel(fn, dim3((unsigned)cus), dim3(kThreads), args, 0, stream);
 }
 
 }  // namespace sx::vf
@@ -716,37 +593,6 @@ int sx_moe_verify_down(const void *h, int64_t M, int64_t A, const int32_t *ids, 
     p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = N, p.K = w->K, p.y = y, p.act = act;
     p.expert_err = expert_err;
     SX_HIP(vf::launch_down(p, stream_of(stream)), fn);
-    return SX_OK;
-}
-
-int sx_moe_verify_ffn(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
-                      const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *gate_up,
-                      const sx_qview *down, int64_t Ew, int32_t *ids, float *coef, void *h, void *y, int act,
-                      uint32_t *router_err, uint32_t *expert_err, uint64_t *sync, sx_stream stream) {
-    const char *fn = "sx_moe_verify_ffn";
-    const int64_t A = k + (shared_logit ? 1 : 0);
-    SX_CHECK(x != nullptr && logits != nullptr && ids != nullptr && coef != nullptr && h != nullptr && y != nullptr &&
-                 router_err != nullptr && expert_err != nullptr && sync != nullptr,
-             fn, " null pointer");
-    if (int rc = check_gate_up(fn, M, A, E, k, Ew, gate_up, act)) return rc;
-    if (int rc = check_down(fn, M, A, Ew, down, act)) return rc;
-    const int64_t I = gate_up->N / Ew / 2, N = down->N / Ew;
-    SX_CHECK(down->K == I, fn, " down K = ", down->K, " is not the gate_up I = ", I);
-    SX_CHECK(ld >= E && (shared_logit == nullptr || shared_ld >= 1), fn, " ld = ", ld, ", shared_ld = ", shared_ld);
-    SX_CHECK(aligned(x, 16) && aligned(h, 16) && aligned(sync, 8), fn, " x, h must be 16-byte, sync 8-byte aligned");
-    SX_CHECK(apart(h, M * A * I * 2, x, M * gate_up->K * 2) && apart(y, M * N * 2, h, M * A * I * 2), fn,
-             " h overlaps x or y");
-    vf::GateUpParams gp{};
-    gp.x = static_cast<const uint16_t *>(x), gp.M = (int)M, gp.A = (int)A, gp.k = (int)k, gp.E = (int)E, gp.Ew = (int)Ew;
-    gp.logits = logits, gp.ld = ld, gp.shared_logit = shared_logit, gp.shared_ld = shared_ld, gp.shared_id = shared_id;
-    gp.q = gate_up->q, gp.scale = gate_up->scale, gp.minv = gate_up->minv, gp.N = gate_up->N / Ew, gp.K = gate_up->K;
-    gp.ids = ids, gp.coef = coef, gp.h = static_cast<uint16_t *>(h), gp.router_err = router_err;
-    gp.expert_err = expert_err;
-    vf::DownParams dp{};
-    dp.h = static_cast<const uint16_t *>(h), dp.M = (int)M, dp.A = (int)A, dp.Ew = (int)Ew, dp.ids = ids, dp.coef = coef;
-    dp.q = down->q, dp.scale = down->scale, dp.minv = down->minv, dp.N = N, dp.K = down->K, dp.y = y, dp.act = act;
-    dp.expert_err = expert_err;
-    SX_HIP(vf::launch_ffn(gp, dp, sync, device_cus(), stream_of(stream)), fn);
     return SX_OK;
 }
 

@@ -43,7 +43,5 @@ struct DownParams {
 
 hipError_t launch_gate_up(const GateUpParams &p, int cus, hipStream_t stream);
 hipError_t launch_down(const DownParams &p, hipStream_t stream);
-// gate_up + down in one cooperative launch of `cus` blocks; sync: the grid barrier's arrival counter
-hipError_t launch_ffn(const GateUpParams &gp, const DownParams &dp, uint64_t *sync, int cus, hipStream_t stream);
 
 }  // namespace sx::vf

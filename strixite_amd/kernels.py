@@ -162,29 +162,6 @@ def verify_down(h, w, ids, coef, Ew, y=None, expert_err=None, stream=None):
     return y, expert_err
 
 
-def verify_ffn(x, logits, gate_up, down, E, k, sync, Ew=None, shared_logit=None, shared_id=0, ids=None, coef=None,
-               h=None, y=None, router_err=None, expert_err=None, stream=None):
-    """verify_gate_up then verify_down in one cooperative launch: ids, coef, h, y. sync: a zeroed int64 device tensor
-    (one element) kept for every call on one stream."""
-    M, ld = x.shape[0], logits.stride(0)
-    Ew = E if Ew is None else Ew
-    A = k + (shared_logit is not None)
-    I, N = gate_up.N // Ew // 2, down.N // Ew
-    dev = x.device
-    ids = torch.empty((M, A), dtype=torch.int32, device=dev) if ids is None else ids
-    coef = torch.empty((M, A), dtype=torch.float32, device=dev) if coef is None else coef
-    h = torch.empty((M, A, I), dtype=x.dtype, device=dev) if h is None else h
-    y = torch.empty((M, N), dtype=x.dtype, device=dev) if y is None else y
-    router_err = _err(dev) if router_err is None else router_err
-    expert_err = _err(dev) if expert_err is None else expert_err
-    assert sync.dtype == torch.int64 and sync.is_cuda
-    sld = 0 if shared_logit is None else shared_logit.stride(0)
-    check(lib().sx_moe_verify_ffn(_p(x), M, _p(logits), ld, E, k, _p(shared_logit), sld, shared_id, gate_up.view(),
-                                  down.view(), Ew, _p(ids), _p(coef), _p(h), _p(y), act_of(x), _p(router_err),
-                                  _p(expert_err), _p(sync), _s(stream)))
-    return ids, coef, h, y, router_err, expert_err
-
-
 def group_routes(ids, E, ws=None, err=None, stream=None):
     M, A = ids.shape
     nb = route_workspace_bytes(M, A, E)

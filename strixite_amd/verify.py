@@ -10,12 +10,12 @@ from . import kernels as kx
 
 class MoeVerifyLayer:
     """One MoE FFN sublayer. Weights: Wr FP32 [E, d], gate_up q4 [E * 2I, d], down q4 [E * d, I] (experts stacked,
-    runtime/qwen4exp.cpp:126-129). At verify width (the shapes kernels.verify_supported takes) two launches: router
-    projection -> routing + gate_up + SwiGLU + down + combine in one cooperative launch (single_launch=False: the last
-    as two launches), the sequence qwen4exp.cpp:1139-1163 runs below kGroupedMinTokens. Otherwise (or fused=False): router projection -> moe_router + moe_group_routes -> grouped
+    runtime/qwen4exp.cpp:126-129). At verify width (the shapes kernels.verify_supported takes) three launches:
+    router projection -> routing + gate_up + SwiGLU -> down + combine (the sequence qwen4exp.cpp:1139-1163 runs below
+    kGroupedMinTokens). Otherwise (or fused=False): router projection -> moe_router + moe_group_routes -> grouped
     gate_up with the SwiGLU epilogue -> grouped down + combine."""
 
-    def __init__(self, Wr, gate_up, down, E, k, max_tokens, act_dtype=torch.bfloat16, fused=True, single_launch=True):
+    def __init__(self, Wr, gate_up, down, E, k, max_tokens, act_dtype=torch.bfloat16, fused=True):
         self.Wr, self.gate_up, self.down, self.E, self.k = Wr, gate_up, down, E, k
         self.d = gate_up.K
         self.I = down.K
@@ -33,8 +33,6 @@ class MoeVerifyLayer:
         self.partial = torch.empty((M * A, self.d), dtype=torch.float32, device=dev)
         self.y = torch.empty((M, self.d), dtype=act_dtype, device=dev)
         self.fused = fused and act_dtype == torch.bfloat16
-        self.single_launch = single_launch
-        self.sync = torch.zeros(1, dtype=torch.int64, device=dev)  # the single launch's grid-barrier counter
 
     def _fused(self, M):
         return self.fused and kx.verify_supported(M, self.k, self.E, self.k, self.E, self.gate_up, self.down)
@@ -44,11 +42,6 @@ class MoeVerifyLayer:
         assert M <= self.M
         ws = self.ws if M == self.M else self.ws[:kx.route_workspace_bytes(M, self.k, self.E) // 4]
         kx.linear_f32w(x, self.Wr, y=self.logits[:M], stream=stream)
-        if self._fused(M) and self.single_launch:
-            kx.verify_ffn(x, self.logits[:M], self.gate_up, self.down, self.E, self.k, self.sync, ids=self.ids[:M],
-                          coef=self.coef[:M], h=self.h[:M], y=self.y[:M], router_err=self.router_err,
-                          expert_err=self.expert_err, stream=stream)
-            return self.y[:M]
         if self._fused(M):
             kx.verify_gate_up(x, self.logits[:M], self.gate_up, self.E, self.k, ids=self.ids[:M], coef=self.coef[:M],
                               h=self.h[:M], router_err=self.router_err, expert_err=self.expert_err, stream=stream)

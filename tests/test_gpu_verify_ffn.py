@@ -65,34 +65,6 @@ def test_verify_ffn_matches_oracle(M, E, k, d, shared):
     assert rerr[0] == 0 and eerr[0] == 0
 
 
-@pytest.mark.parametrize("M,E,k,d,shared", [(6, 64, 10, 512, False), (1, 16, 4, 1024, False), (16, 40, 3, 512, True),
-                                            (5, 300, 8, 2048, True), (4, 1000, 16, 512, False)])
-def test_single_launch_matches_two_launches(M, E, k, d, shared):
-    """sx_moe_verify_ffn (one cooperative launch, a grid barrier between the phases) gives the two launches' ids,
-    coef, h and y bit for bit, on three calls in a row with one barrier counter (the second with fewer tokens)."""
-    import torch
-    I = 1024
-    Ew = E + (1 if shared else 0)
-    wgu, wdn, rng = make(M * 11 + E, Ew, I, d)
-    Wgu, Wdn = kx().QWeight.upload(wgu), kx().QWeight.upload(wdn)
-    counter = torch.zeros(1, dtype=torch.int64, device="cuda")
-    for Mc in (M, max(1, M - 3), M):
-        x = util.bf16_dev(util.f32_to_bf16(rng.standard_normal((Mc, d)).astype(np.float32)))
-        Ld = util.f32_dev((rng.standard_normal((Mc, Ew)) * 1.3).astype(np.float32))
-        sl = Ld[:, E:] if shared else None
-        ids, coef, h, rerr, eerr = kx().verify_gate_up(x, Ld, Wgu, E, k, Ew=Ew, shared_logit=sl, shared_id=E)
-        y, _ = kx().verify_down(h, Wdn, ids, coef, Ew, expert_err=eerr)
-        ids1, coef1, h1, y1, rerr1, eerr1 = kx().verify_ffn(x, Ld, Wgu, Wdn, E, k, counter, Ew=Ew, shared_logit=sl,
-                                                            shared_id=E)
-        sync()
-        assert torch.equal(ids, ids1) and torch.equal(coef, coef1)
-        assert torch.equal(h.view(torch.int16), h1.view(torch.int16))
-        assert torch.equal(y.view(torch.int16), y1.view(torch.int16))
-        assert list(eerr1.cpu().numpy()[:3]) == [0, 0, 0] and list(rerr1.cpu().numpy()[:3]) == [0, 0, 0]
-    # one arrival a block a launch, the grid being one block a CU
-    assert int(counter.item()) == 3 * torch.cuda.get_device_properties(0).multi_processor_count
-
-
 def test_verify_ffn_nonfinite_logit_matches_per_slot_path():
     """A NaN logit fails its token in the router (ids -1, coef NaN, router error); the experts then see bad ids:
     NaN h rows for those slots, a NaN y row for the token and the expert error of its first slot - the same words and
