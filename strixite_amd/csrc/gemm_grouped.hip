@@ -156,8 +156,11 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     const bool two_tb = T > 32;  // the second 32-slot half holds slots (uniform)
 
     // K step k (clamped: past the end it re-loads the last step, never used) into stage st
+    // (a tile of at most 32 slots leaves rows 32..63 alone: waves 2 and 3, which cover them, load nothing)
+    const bool dma_on = two_tb || wave < 2;  // wave-uniform
     auto issue_x = [&](int kstep, int st) __attribute__((always_inline)) {
         const int k = min(kstep, nk - 1);
+        if (!dma_on) return;
 #pragma unroll
         for (int i = 0; i < kDmaPerWave; ++i)
             dma16(xl[i] + (int64_t)k * kSpan, xs_at(st) + (kDmaPerWave * wave + i) * 1024);
@@ -181,6 +184,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     // the span sums of stage st's 64 rows (K step grp): 4 threads a row, 4 slots each (any slot order sums the row)
     auto sum_rows = [&](int st, int grp) __attribute__((always_inline)) {
         const int r = tid >> 2, qd = tid & 3;
+        if (!dma_on) return;  // rows 32..63 of a tile of at most 32 slots
         const unsigned char *xb = xs_at(st) + r * 256 + qd * 64;
         // read in asm: the wait-count pass would otherwise hold these reads for every DMA in flight (it cannot
         // tell this stage from the one just issued); the step's barrier already covers this stage's DMA
@@ -275,7 +279,11 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     //   every wave is done with step k - 1 (stage (k + 3) % 4 is free) and sees the DMA of k + 1 and the sums of k.
     auto step = [&](int k, auto st_tag, auto rs_tag, auto two_tag) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_tag)::value;
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kLoadsPerStep) : "memory");
+        if (dma_on)
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kLoadsPerStep) : "memory");
+        else  // no DMA a step: the same loads are this many fewer issues back
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kLoadsPerStep - kDmaPerWave)
+                         : "memory");
         issue_x(k + 3, (ST + 3) % kStages);
         __builtin_amdgcn_sched_barrier(0);
         sum_rows((ST + 1) % kStages, k + 1);
