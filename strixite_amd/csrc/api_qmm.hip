@@ -3,6 +3,7 @@
 // moe_grouped.hip:476-556); the work runs in qmm_impl.hpp.
 #include "common.hpp"
 #include "gemm_grouped.hpp"
+#include "dense_ks.hpp"
 #include "qmm.hpp"
 
 namespace sx {
@@ -80,6 +81,12 @@ int linear(const char *fn, int bits, const void *x, const sx_qview *w, void *y, 
              " with input ", act, " unsupported (same dtype, or BF16 -> F32)");
     SX_CHECK(apart(x, M * w->K * act_bytes(act), y, M * w->N * act_bytes(out_act)), fn, " output y [", y, ", +",
              M * w->N * act_bytes(out_act), " B) overlaps input x [", x, ", +", M * w->K * act_bytes(act), " B)");
+    if (dks::eligible(bits, w->G, w->N, w->K, M, act, out_act, device_cus())) {  // few tiles: K split over the waves
+        dks::Params d{};
+        d.x = x, d.q = w->q, d.scale = w->scale, d.minv = w->minv, d.y = y, d.M = (int)M, d.N = w->N, d.K = w->K;
+        SX_HIP(dks::launch(bits, act, out_act, d, device_cus(), stream_of(stream)), fn);
+        return SX_OK;
+    }
     const int nsplit = act == SX_ACT_F32 ? 3 : 1;
     const int rows = rows_that_fit(bits, nsplit, w->K, w->G, (int)(M < 16 ? M : 16));
     SX_CHECK(qmm::lds_bytes(bits, nsplit, w->K, w->G, rows, 1) <= 160 * 1024, fn, " K = ", w->K,

@@ -52,6 +52,18 @@ def test_config2_verify_width(bits, G):
     util.assert_close(got, ref, what=f"config 2 q{bits}")
 
 
+@pytest.mark.parametrize("bits,K", [(4, 512), (4, 1024), (4, 4096), (4, 8192), (8, 256), (8, 1024), (8, 4096)])
+@pytest.mark.parametrize("M,act,out_act", [(1, F32, F32), (5, BF16, BF16), (16, BF16, F32), (3, F32, F32)])
+def test_linear_k_split_path(bits, K, M, act, out_act):
+    """The decode / verify-width kernel (K split over a block's waves, dense_ks.hip) on the shapes it takes - q4 G = 128
+    and q8 G = 64 with 4 .. 64 spans, M <= 16, at most a 16-row tile a block - and its neighbours the general kernel
+    takes (FP32 x too long for its LDS, more tiles than blocks): a partial last tile, a run of tiles a block."""
+    G = 128 if bits == 4 else 64
+    N = 3000 if K == 1024 else 200
+    got, ref = run(bits, N, K, G, M, act, out_act, seed=K + M)
+    util.assert_close(got, ref, what=f"q{bits} K{K} M{M} act {act}->{out_act}")
+
+
 def test_linear_rejects_misaligned_x():
     import torch
     from strixite_amd import kernels as kx, SxError
