@@ -12,6 +12,8 @@
 #include "dense_ks.hpp"
 #include "qmm_impl.hpp"
 
+#include <atomic>
+
 namespace sx::dks {
 namespace {
 
@@ -207,12 +209,14 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
 template <int BITS, int NPL, int SPW, typename TX, typename TY>
 hipError_t go(const Params &p, int cus, size_t lds, hipStream_t stream) {
     auto fn = dense_ks_kernel<BITS, NPL, SPW, TX, TY>;
-    static bool sized = false;  // the dynamic LDS limit, once an instantiation (every launch asks for <= kLdsMax)
-    if (!sized) {
+    // the dynamic LDS limit, set once an instantiation (every launch asks for <= kLdsMax; setting it twice from two
+    // threads is harmless)
+    static std::atomic<bool> sized{false};
+    if (!sized.load(std::memory_order_acquire)) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
         if (e != hipSuccess) return e;
-        sized = true;
+        sized.store(true, std::memory_order_release);
     }
     hipLaunchKernelGGL(fn, dim3((unsigned)cus), dim3(kThreads), lds, stream, p);
     return hipGetLastError();
