@@ -69,6 +69,41 @@ __global__ void __launch_bounds__(256) combine_reduce_kernel(const float *partia
     }
 }
 
+// The same sums four outputs a thread (N a multiple of 4, 16-byte aligned partials): a block row is one token, the
+// A partial rows' float4 loads go out eight at a time before their FMAs, which run in slot order as above (the
+// same value bit for bit), and no 64-bit division a value.
+template <typename T>
+__global__ void __launch_bounds__(256) combine_reduce4_kernel(const float *partial, const int32_t *ids,
+                                                              const float *coef, int64_t A, int64_t E, int64_t N,
+                                                              T *y) {
+    constexpr int kBatch = 8;
+    const int64_t m = blockIdx.y;
+    const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (n >= N) return;
+    const float *prow = partial + m * A * N + n;
+    bool ok = true;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t a0 = 0; a0 < A; a0 += kBatch) {
+        float4 pv[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {  // clamped: rows past A load row A - 1 and are not used
+            const int64_t a = a0 + b < A ? a0 + b : A - 1;
+            pv[b] = *reinterpret_cast<const float4 *>(prow + a * N);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            if (a0 + b >= A) break;
+            const int32_t id = ids[m * A + a0 + b];
+            ok = ok && id >= 0 && id < E;
+            const float c = coef[m * A + a0 + b];
+            v[0] = fmaf(c, pv[b].x, v[0]), v[1] = fmaf(c, pv[b].y, v[1]);
+            v[2] = fmaf(c, pv[b].z, v[2]), v[3] = fmaf(c, pv[b].w, v[3]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_act(y, m * N + n + j, ok ? v[j] : qnan());
+}
+
 // ---------------- swiglu ----------------
 
 template <typename T>
@@ -120,6 +155,16 @@ Layout layout_of(int64_t M, int64_t A, int64_t E) {
 
 int combine_reduce(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                    int64_t N, void *y, int act, hipStream_t stream) {
+    if (N % 4 == 0 && aligned(partial, 16) && (N / 4 + 255) / 256 <= 0x7fffffff && M <= 65535) {
+        const dim3 grid((unsigned)((N / 4 + 255) / 256), (unsigned)M);
+        if (act == SX_ACT_F32)
+            combine_reduce4_kernel<float><<<grid, 256, 0, stream>>>(partial, ids, coef, A, E, N, static_cast<float *>(y));
+        else
+            combine_reduce4_kernel<uint16_t><<<grid, 256, 0, stream>>>(partial, ids, coef, A, E, N,
+                                                                       static_cast<uint16_t *>(y));
+        SX_LAUNCHED("combine_reduce M=", M, " A=", A, " N=", N);
+        return SX_OK;
+    }
     const int blocks = grid_for(M * N, 8192);
     if (act == SX_ACT_F32)
         combine_reduce_kernel<float><<<blocks, 256, 0, stream>>>(partial, ids, coef, M, A, E, N, static_cast<float *>(y));

@@ -315,3 +315,26 @@ def test_config3_moe_verify_layer_full_size():
     flips = int((np.sort(o_ids, 1) != np.sort(ids, 1)).any(1).sum())
     print(f"config3: U = {U} distinct experts; tokens whose routing flips from CPU logits: {flips}")
     assert flips <= 1
+
+
+@pytest.mark.parametrize("d", [42, 4096])
+def test_combine_grouped_row_counts(d):
+    """combine_grouped's reduce over the slot partials: four outputs a thread when the row count allows (d a multiple
+    of 4), one otherwise (d = 42), against the oracle's combine, with an invalid id's token NaN."""
+    import torch
+    M, A, E, I = 37, 3, 6, 128
+    rng = np.random.default_rng(d)
+    wdn = util.rand_qweight(rng, 4, E * d, I, 128)
+    h = util.f32_to_bf16(rng.standard_normal((M, A, I)).astype(np.float32))
+    ids = np.stack([rng.choice(E, A, replace=False) for _ in range(M)]).astype(np.int32)
+    ids[5, 1] = E + 2
+    coef = rng.random((M, A)).astype(np.float32)
+    ids_d = torch.from_numpy(ids).cuda()
+    ws, err = kx().group_routes(ids_d, E)
+    y = kx().combine_grouped(util.bf16_dev(h), kx().QWeight.upload(wdn), E, ids_d, util.f32_dev(coef), ws)
+    sync()
+    yh = util.host_bits(y)
+    assert np.isnan(util.as_f32(yh[5])).all()
+    ok = [m for m in range(M) if m != 5]
+    ref_y, _ = orc.experts_combine(h[ok], wdn, E, ids[ok], coef[ok])
+    util.assert_close(yh[ok], ref_y, what=f"combine_grouped d={d}")
