@@ -108,11 +108,15 @@ __global__ void __launch_bounds__(256) linear_f32w_kernel(const TX *x, const flo
 // ---------------- router projection at prefill width (M >= 64, BF16 x): MFMA ----------------
 // Each FP32 weight is the exact sum of three BF16 terms (hi = rne(w), mid = rne(w - hi), lo = rne(w - hi - mid)), so
 // x . W = x . hi + x . mid + x . lo with every product exact in v_mfma_f32_16x16x32_bf16 and FP32 accumulation, as
-// the scalar kernel's. A wave owns 16 weight rows x 64 tokens (4 MFMA tiles sharing each split weight fragment); a
-// block 64 rows x 64 tokens. The weight is read once per 64 tokens instead of once per 8.
+// the scalar kernel's. A block owns 64 weight rows x 64 tokens; a wave 16 rows x the 64 tokens (4 MFMA tiles sharing
+// each split weight fragment). The block's 64 activation rows of a K step (4 KB) are loaded once, a 16-byte chunk a
+// thread, and shared through a double-buffered LDS tile (rows 80 bytes apart: the operand reads are free of bank
+// conflicts), so the activations are read once per 64 weight rows rather than once per wave.
 typedef __bf16 pw_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pw_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pw_u32x4 __attribute__((ext_vector_type(4)));  // a vector, not an aggregate: copies stay in registers
 constexpr int kPwTok = 64, kPwRows = 64, kPwMinTokens = 64;
+constexpr int kPwLd = 40;  // BF16 a token row of the LDS tile (32 of the step + 8 of padding)
 
 __device__ __forceinline__ void split3(const float4 &a, const float4 &b, pw_bf16x8 &hi, pw_bf16x8 &mid, pw_bf16x8 &lo) {
     // hardware RNE conversions (v_cvt_pk_bf16_f32); the weights are finite, so NaN payloads never matter here
@@ -128,48 +132,60 @@ __device__ __forceinline__ void split3(const float4 &a, const float4 &b, pw_bf16
 
 __global__ void __launch_bounds__(256) linear_f32w_mfma_kernel(const uint16_t *x, const float *W, float *y, int64_t M,
                                                                int64_t N, int64_t K) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n16 = lane & 15, g = lane >> 4;
+    __shared__ __attribute__((aligned(16))) uint16_t xt[2][kPwTok * kPwLd];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
     const int64_t row = (int64_t)blockIdx.x * kPwRows + wave * 16 + n16, t0 = (int64_t)blockIdx.y * kPwTok;
     const float *wr = W + min(row, N - 1) * K + g * 8;
-    const uint16_t *xr[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) xr[tt] = x + min(t0 + tt * 16 + n16, M - 1) * K + g * 8;
+    // this thread's chunk of every step's activation tile: token tid / 4 (clamped), 16 bytes at (tid % 4) * 8
+    const uint16_t *xc = x + min(t0 + tid / 4, M - 1) * K + (tid % 4) * 8;
+    const int xs_off = (tid / 4) * kPwLd + (tid % 4) * 8;
     pw_f32x4 acc[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) acc[tt] = pw_f32x4{0.f, 0.f, 0.f, 0.f};
     // kPwDepth K steps of loads in flight: step s + kPwDepth is issued into the slot step s frees (K steps past the
-    // end re-load the last step, never used).
+    // end re-load the last step, never used)
     constexpr int kPwDepth = 4;
     const int nk = (int)(K / 32);
     float4 wb[kPwDepth][2];
-    pw_bf16x8 ab[kPwDepth][4];
-    auto issue = [&](int step, int slot) {
+    pw_u32x4 xb[kPwDepth];
+    auto issue = [&](int step, int slot) __attribute__((always_inline)) {
         const int64_t k0 = (int64_t)min(step, nk - 1) * 32;
         wb[slot][0] = *reinterpret_cast<const float4 *>(wr + k0), wb[slot][1] = *reinterpret_cast<const float4 *>(wr + k0 + 4);
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) ab[slot][tt] = *reinterpret_cast<const pw_bf16x8 *>(xr[tt] + k0);
+        xb[slot] = *reinterpret_cast<const pw_u32x4 *>(xc + k0);
     };
 #pragma unroll
     for (int d = 0; d < kPwDepth; ++d) issue(d, d);
-    for (int s0 = 0; s0 < nk; s0 += kPwDepth) {
+    // one K step on ring slot D (a constant: the slots stay in registers)
+    auto step = [&](int s0, auto d_tag) __attribute__((always_inline)) {
+        constexpr int D = decltype(d_tag)::value, BUF = D & 1;  // kPwDepth is even: the LDS buffer of step s0 + D
+        // the slot's activation chunk into LDS and its weights split before the slot is reloaded (a value still live
+        // at the reload would make the loop rotate the ring through copies that wait for every load)
+        *reinterpret_cast<pw_u32x4 *>(&xt[BUF][xs_off]) = xb[D];
+        pw_bf16x8 hi, mid, lo;
+        split3(wb[D][0], wb[D][1], hi, mid, lo);
+        __builtin_amdgcn_sched_barrier(0);  // the reload stays after the last use of the slot
+        issue(s0 + D + kPwDepth, D);
+        // the tile of this step is complete; the other buffer's reads (the step before) are done. LDS-only fences:
+        // a __syncthreads() would also wait for the loads of the steps in flight.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        if (s0 + D < nk) {  // uniform
 #pragma unroll
-        for (int d = 0; d < kPwDepth; ++d) {
-            const float4 wa = wb[d][0], wc = wb[d][1];
-            pw_bf16x8 A[4];
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) A[tt] = ab[d][tt];
-            issue(s0 + d + kPwDepth, d);
-            if (s0 + d < nk) {  // uniform
-                pw_bf16x8 hi, mid, lo;
-                split3(wa, wc, hi, mid, lo);
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt) {
-                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[tt], lo, acc[tt], 0, 0, 0);
-                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[tt], mid, acc[tt], 0, 0, 0);
-                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[tt], hi, acc[tt], 0, 0, 0);
-                }
+            for (int tt = 0; tt < 4; ++tt) {
+                const pw_bf16x8 A = *reinterpret_cast<const pw_bf16x8 *>(&xt[BUF][(tt * 16 + n16) * kPwLd + g * 8]);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, lo, acc[tt], 0, 0, 0);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, mid, acc[tt], 0, 0, 0);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, hi, acc[tt], 0, 0, 0);
             }
         }
+    };
+    static_assert(kPwDepth == 4, "the K loop below is unrolled by four");
+    for (int s0 = 0; s0 < nk; s0 += kPwDepth) {
+        step(s0, std::integral_constant<int, 0>{});
+        step(s0, std::integral_constant<int, 1>{});
+        step(s0, std::integral_constant<int, 2>{});
+        step(s0, std::integral_constant<int, 3>{});
     }
     if (row >= N) return;
 #pragma unroll
