@@ -35,6 +35,8 @@ def parse():
     ap.add_argument("--probe", action="store_true",
                     help="for rocprofv3 --pmc: a plain copy kernel of known size (the counters' calibration), then the "
                          "config-3 gate_up and down kernels alone, and exit")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only config 4's prefill layer (for rocprofv3 runs): one JSON line with its timings")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two --probe counter runs (FETCH_SIZE, WRITE_SIZE) into " + TRAFFIC_JSON)
     return ap.parse_args()
@@ -393,6 +395,9 @@ def main():
     strixite_amd.lib()  # fails loudly without the built library
     if args.probe:
         probe()
+        return
+    if args.prefill_only:
+        print(json.dumps({"cfg4_prefill_layer": prefill_layer()}))
         return
 
     out = {"metric": METRIC, "value": None, "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
