@@ -35,6 +35,13 @@ __device__ __forceinline__ float load_act(const uint16_t *p, int64_t i) { return
 __device__ __forceinline__ float as_stored(float v, const float *) { return v; }
 __device__ __forceinline__ float as_stored(float v, const uint16_t *) { return as_bf16(v); }
 
+// A block barrier ordering LDS accesses only: __syncthreads() would also wait for every global load in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float qnan() { return __uint_as_float(0x7fc00000u); }
 
 // SiLU in the reference's form v / (1 + exp(-v)) (kernels/swiglu.hip:19).

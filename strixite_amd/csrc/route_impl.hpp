@@ -26,29 +26,31 @@ __device__ __forceinline__ float key_value(uint64_t key) {
 // [1,0,3,2], quad [2,3,0,1], half-row mirror and row mirror leave every lane with its row's result (max, min and
 // sum need no particular pairing); then row_bcast:15 (rows 1, 3 take lane 15 of the row before) and row_bcast:31
 // (rows 2, 3 take lane 31) leave the wave's result in lane 63, read out as a scalar. A row outside a broadcast's row
-// mask receives `old`: the value itself for max / min, 0 for sum.
+// mask receives `old`: the operation's identity.
 template <int CTRL, int ROWS = 0xF>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xF, false);
 }
 
+// `old` is the operation's identity (0 for max, ~0 for min), so the compiler folds each move into the max / min
+// as one DPP instruction.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, dpp_u32<0xB1>(v, v));
-    v = max(v, dpp_u32<0x4E>(v, v));
-    v = max(v, dpp_u32<0x141>(v, v));
-    v = max(v, dpp_u32<0x140>(v, v));
-    v = max(v, dpp_u32<0x142, 0xA>(v, v));
-    v = max(v, dpp_u32<0x143, 0xC>(v, v));
+    v = max(v, dpp_u32<0xB1>(0u, v));
+    v = max(v, dpp_u32<0x4E>(0u, v));
+    v = max(v, dpp_u32<0x141>(0u, v));
+    v = max(v, dpp_u32<0x140>(0u, v));
+    v = max(v, dpp_u32<0x142, 0xA>(0u, v));
+    v = max(v, dpp_u32<0x143, 0xC>(0u, v));
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-    v = min(v, dpp_u32<0xB1>(v, v));
-    v = min(v, dpp_u32<0x4E>(v, v));
-    v = min(v, dpp_u32<0x141>(v, v));
-    v = min(v, dpp_u32<0x140>(v, v));
-    v = min(v, dpp_u32<0x142, 0xA>(v, v));
-    v = min(v, dpp_u32<0x143, 0xC>(v, v));
+    v = min(v, dpp_u32<0xB1>(~0u, v));
+    v = min(v, dpp_u32<0x4E>(~0u, v));
+    v = min(v, dpp_u32<0x141>(~0u, v));
+    v = min(v, dpp_u32<0x140>(~0u, v));
+    v = min(v, dpp_u32<0x142, 0xA>(~0u, v));
+    v = min(v, dpp_u32<0x143, 0xC>(~0u, v));
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 

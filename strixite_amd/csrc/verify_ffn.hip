@@ -43,44 +43,54 @@ struct Routes {                // one block's copy of the routing (LDS)
     uint32_t u_mask[kMaxSlots];  // their tokens (bit m)
     int U;
     uint64_t bad_slots;        // invalid slots: id outside [0, Ew) or repeated within its token
-    int wtot[kWaves][3];
     int8_t slot_tab[kMaxSlots][kMaxTokens];  // [unit][token]: the token's slot of the unit's expert, or -1
 };
 
 // The distinct experts of the slots in id order with their token masks. bad_slots marks ids outside [0, Ew) and
-// repeats of an id within a token (the routers never produce one; such a slot is treated as invalid).
-// emask: LDS [Ew]. Expects R.ids written and a barrier since; ends with a barrier.
-__device__ void build_units(Routes &R, uint32_t *emask, int S, int A, int Ew) {
+// repeats of an id within a token (the routers never produce one; such a slot is treated as invalid: the later
+// slot of the two). Wave 0 alone does it, from `id` = its lane's slot id (lane < S): the LDS operations of one wave
+// take effect in program order, so no barrier is needed until the closing one. Experts go by passes of 64 (pass j:
+// experts 64 j + lane), a ballot and its lane count placing each pass's units after the previous pass's.
+// emask: LDS [kMaxExperts]. Ends with an LDS-only block barrier.
+__device__ void build_units(Routes &R, uint32_t *emask, int32_t id, int S, int A, int Ew) {
+    constexpr int kPass = kMaxExperts / 64;
     const int t = threadIdx.x;
-    for (int e = t; e < Ew; e += kThreads) emask[e] = 0;
     if (t < 64) {
-        bool bad = false;
-        if (t < S) {
-            const int32_t id = R.ids[t];
-            bad = !(id >= 0 && id < Ew);
-            for (int s = t - t % A; s < t; ++s) bad |= R.ids[s] == id;
+        const int passes = (Ew + 63) >> 6;
+#pragma unroll
+        for (int j = 0; j < kPass; ++j)
+            if (j < passes) emask[64 * j + t] = 0u;
+        static_assert(kMaxSlots * kMaxTokens == 64 * 16, "slot_tab: one 16-byte row a lane");
+        reinterpret_cast<int4 *>(&R.slot_tab[0][0])[t] = make_int4(-1, -1, -1, -1);
+        const bool in = t < S;
+        bool bad = in && !(id >= 0 && id < Ew);
+        const uint32_t bit = in ? 1u << (t / A) : 0u;
+        uint32_t old = 0u;
+        if (in && !bad) old = atomicOr(&emask[id], bit);
+        if (__ballot(old & bit)) {  // a repeat within a token: mark the later slots exactly
+            for (int j = 1; j < A; ++j) {
+                const int32_t o = __shfl(id, max(t - j, 0));
+                bad |= in && t % A >= j && o == id;
+            }
         }
-        const uint64_t mask = __ballot(bad);
-        if (t == 0) R.bad_slots = mask;
+        const uint64_t bad_mask = __ballot(bad);
+        uint32_t mk[kPass];
+#pragma unroll
+        for (int j = 0; j < kPass; ++j) mk[j] = j < passes ? emask[64 * j + t] : 0u;
+        int base = 0;
+#pragma unroll
+        for (int j = 0; j < kPass; ++j) {
+            if (j >= passes) break;
+            const uint64_t bal = __ballot(mk[j] != 0u);
+            const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (mk[j]) R.u_exp[pos] = 64 * j + t, R.u_mask[pos] = mk[j], emask[64 * j + t] = (uint32_t)pos;
+            base += __popcll(bal);
+        }
+        if (t == 0) R.U = base, R.bad_slots = bad_mask;
+        if (in && !bad) R.slot_tab[emask[id]][t / A] = (int8_t)t;
     }
-    __syncthreads();
-    if (t < S && !((R.bad_slots >> t) & 1ull)) atomicOr(&emask[R.ids[t]], 1u << (t / A));
-    __syncthreads();
-    const int per = (Ew + kThreads - 1) / kThreads;
-    const int b0 = min(t * per, Ew), b1 = min(b0 + per, Ew);
-    int v[3] = {0, 0, 0}, ex[3], tot[3];
-    for (int b = b0; b < b1; ++b) v[0] += emask[b] != 0;
-    routing::block_scan3<kThreads>(v, ex, tot, R.wtot);
-    int pos = ex[0];
-    for (int b = b0; b < b1; ++b) {  // emask[b] becomes the unit index of expert b (read only for valid slots)
-        const uint32_t mk = emask[b];
-        if (mk) R.u_exp[pos] = b, R.u_mask[pos] = mk, emask[b] = pos++;
-    }
-    if (t == 0) R.U = tot[0];
-    for (int i = t; i < kMaxSlots * kMaxTokens; i += kThreads) (&R.slot_tab[0][0])[i] = -1;
-    __syncthreads();
-    if (t < S && !((R.bad_slots >> t) & 1ull)) R.slot_tab[emask[R.ids[t]]][t / A] = (int8_t)t;
-    __syncthreads();
+    lds_barrier();  // the loads in flight (activations, weights) keep going
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -131,8 +141,8 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
         routing::route_values<NV>(v1, p.E, p.k, p.shared_logit != nullptr, sl1, p.shared_id, wave + kWaves,
                                   R.ids + (wave + kWaves) * A, R.coef + (wave + kWaves) * A, nullptr,
                                   lead ? p.router_err : nullptr);
-    __syncthreads();
-    build_units(R, emask, S, A, Ew);
+    lds_barrier();
+    build_units(R, emask, tid < S ? R.ids[tid] : 0, S, A, Ew);
     const int U = __builtin_amdgcn_readfirstlane(R.U);
     const int64_t Nrows = p.N / 2, rowbytes = K / 2, ngroups = K / kSpan;
     if (lead) {
@@ -338,8 +348,7 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     }
     R.ids[lane] = my_id, R.coef[lane] = my_coef;  // every wave the same values (unconditional: nothing sinks the loads)
     for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(zero_block)[i] = 0u;
-    __syncthreads();
-    build_units(R, emask, S, A, Ew);
+    build_units(R, emask, my_id, S, A, Ew);  // its closing barrier also covers ids, coef and the zero block
     const int U = __builtin_amdgcn_readfirstlane(R.U);
     const uint64_t bad_slots = R.bad_slots;
     if (blockIdx.x == 0 && bad_slots && tid == 0) {
@@ -402,7 +411,7 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
             if ((c8 & 15) == 0) hsum[r * nspan + (c8 >> 4)] = sum;
         }
     }
-    __syncthreads();
+    lds_barrier();  // the ring's weight loads stay in flight
 
     // consume: per item, A row n16 = token n16's slot of the unit's expert (or zeros); D rows 4g + v = tokens
     float yacc[4] = {0.f, 0.f, 0.f, 0.f};
