@@ -126,13 +126,14 @@ def moe_layer_bench(args, out):
 
     # dominant kernel alone: routing + gate_up + SwiGLU (the layer's second launch) over the same rotating batches
     h = torch.empty((M, k, I), dtype=torch.bfloat16, device="cuda")
+    h_sums = torch.empty((M * k, I // 16), dtype=torch.float32, device="cuda")
     ids_b = torch.empty((M, k), dtype=torch.int32, device="cuda")
     coef_b = torch.empty((M, k), dtype=torch.float32, device="cuda")
     rerr, eerr = torch.zeros(4, dtype=torch.int32, device="cuda"), torch.zeros(4, dtype=torch.int32, device="cuda")
 
     def gate_up(i):
         kx.verify_gate_up(xs[i % R], routes[i % R][3], gu, E, k, ids=ids_b, coef=coef_b, h=h, router_err=rerr,
-                          expert_err=eerr)
+                          expert_err=eerr, h_sums=h_sums)
 
     n = max(args.steps, 64)
     ms = time_launches(gate_up, n)
@@ -150,10 +151,11 @@ def moe_layer_bench(args, out):
 
     # the down projection + combine (the layer's third launch), alone
     hh = [torch.randn((M, k, I), device="cuda").to(torch.bfloat16) for _ in range(R)]
+    hs = [t.float().view(M * k, I // 16, 16).sum(-1) for t in hh]  # the 16-feature sums gate_up hands over
     yb = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
 
     def down(i):
-        kx.verify_down(hh[i % R], dn, routes[i % R][0], routes[i % R][1], E, y=yb, expert_err=eerr)
+        kx.verify_down(hh[i % R], dn, routes[i % R][0], routes[i % R][1], E, y=yb, expert_err=eerr, h_sums=hs[i % R])
 
     ms_dn = time_launches(down, n)
     dn_bytes = sum(down_bytes(Us[i % R], dn.nbytes() // E, M, d, k, I) for i in range(n)) / n
@@ -329,14 +331,15 @@ def probe():
         routes.append((layer.ids.clone(), layer.coef.clone(), layer.logits.clone()))
         Us.append(int(torch.unique(routes[-1][0]).numel()))
     h = torch.empty((M, k, I), dtype=torch.bfloat16, device="cuda")
+    h_sums = torch.empty((M * k, I // 16), dtype=torch.float32, device="cuda")
     ids_b = torch.empty((M, k), dtype=torch.int32, device="cuda")
     coef_b = torch.empty((M, k), dtype=torch.float32, device="cuda")
     yb = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
     torch.cuda.synchronize()
     for i in range(R):
-        kx.verify_gate_up(xs[i], routes[i][2], gu, E, k, ids=ids_b, coef=coef_b, h=h)
+        kx.verify_gate_up(xs[i], routes[i][2], gu, E, k, ids=ids_b, coef=coef_b, h=h, h_sums=h_sums)
     for i in range(R):
-        kx.verify_down(h, dn, routes[i][0], routes[i][1], E, y=yb)
+        kx.verify_down(h, dn, routes[i][0], routes[i][1], E, y=yb, h_sums=h_sums)
     torch.cuda.synchronize()
     alg = {"gate_up": sum(gate_up_bytes(U, gu.nbytes() // E, M, d, E, k, I) for U in Us) / R,
            "down": sum(down_bytes(U, dn.nbytes() // E, M, d, k, I) for U in Us) / R}

@@ -102,14 +102,17 @@ int sx_moe_router_group(const void *logits, int64_t ld, int64_t M, int64_t E, in
 int sx_moe_verify_supported(int64_t M, int64_t A, int64_t E, int64_t k, int64_t Ew, const sx_qview *gate_up,
                             const sx_qview *down, int act);
 /* route (ids, coef [M, A]; router_err) + h [M, A, I] = silu(x W_gate^T) * (x W_up^T) per slot (expert_err, NaN rows
- * for invalid slots). shared_logit nullable. */
+ * for invalid slots). shared_logit nullable. h_sums (nullable, 16-byte aligned): FP32 [M * A, ceil(I / 16)], the sum
+ * of each 16-feature run of the valid slots' h rows as stored, for sx_moe_verify_down. */
 int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
                           const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *gate_up,
-                          int64_t Ew, int32_t *ids, float *coef, void *h, int act, uint32_t *router_err,
-                          uint32_t *expert_err, sx_stream stream);
-/* y [M, N] = sum_a coef[m, a] * (h[m, a] W_down[ids[m, a]]^T); NaN rows for tokens with an invalid slot. */
-int sx_moe_verify_down(const void *h, int64_t M, int64_t A, const int32_t *ids, const float *coef,
-                       const sx_qview *down, int64_t Ew, void *y, int act, uint32_t *expert_err, sx_stream stream);
+                          int64_t Ew, int32_t *ids, float *coef, void *h, float *h_sums, int act,
+                          uint32_t *router_err, uint32_t *expert_err, sx_stream stream);
+/* y [M, N] = sum_a coef[m, a] * (h[m, a] W_down[ids[m, a]]^T); NaN rows for tokens with an invalid slot. h_sums
+ * (nullable): the h_sums sx_moe_verify_gate_up wrote with this h (saves the kernel summing h itself). */
+int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A, const int32_t *ids,
+                       const float *coef, const sx_qview *down, int64_t Ew, void *y, int act, uint32_t *expert_err,
+                       sx_stream stream);
 /* y [M, A, N] (linear_q4_experts_gather_grouped, moe_grouped.hpp:53-55). */
 int sx_linear_q4_experts_gather_grouped(const void *x, const sx_qview *w, int64_t E, const void *ws, size_t ws_bytes,
                                         int64_t M, int64_t A, void *y, int act, int math, sx_stream stream);

@@ -67,8 +67,9 @@ SIGNATURES = {
     "sx_linear_f32w": [_P, _P, _I64, _I64, _P, _I64, _INT, _P],
     "sx_moe_router_group": [_P, _I64, _I64, _I64, _I64, _INT, _P, _P, _P, _P, ctypes.c_size_t, _P, _P],
     "sx_moe_verify_supported": [_I64, _I64, _I64, _I64, _I64, _QV, _QV, _INT],
-    "sx_moe_verify_gate_up": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _INT, _QV, _I64, _P, _P, _P, _INT, _P, _P, _P],
-    "sx_moe_verify_down": [_P, _I64, _I64, _P, _P, _QV, _I64, _P, _INT, _P, _P],
+    "sx_moe_verify_gate_up": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _INT, _QV, _I64, _P, _P, _P, _P, _INT, _P, _P,
+                              _P],
+    "sx_moe_verify_down": [_P, _P, _I64, _I64, _P, _P, _QV, _I64, _P, _INT, _P, _P],
     "sx_logits_topk_workspace_bytes": [_I64, _I64, _I64, _SZP],
     "sx_logits_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_size_t, _P, _I64, _P],
     "sx_mtp_pick": [_P, _I64, _P, _P, _P, _P, _P, _P],

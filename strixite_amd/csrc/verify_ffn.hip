@@ -239,18 +239,25 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
     constexpr int VS = Q >= 4 ? 1 : 4 / Q;
     const int vb = Q == 8 ? kq >> 1 : kq * VS;
     const bool st_lane = Q != 8 || (g & 1) == (kq & 1);
+    // Called by whole waves (the item is wave-uniform): the 16 lanes of a row (one g) hold the tile's 16 features
+    // of token r, and their sum of the stored values is the slot's h_sums entry for the tile.
     auto epilogue = [&](int item, const float (&gate)[VS], const float (&up)[VS]) __attribute__((always_inline)) {
         const int u = item / T16, tile = item - u * T16;
         const uint32_t mask = R.u_mask[u];
         const int64_t n = (int64_t)tile * 16 + n16;
-        if (n >= Nrows || !st_lane) return;
+        const bool n_in = n < Nrows;
 #pragma unroll
         for (int j = 0; j < VS; ++j) {
             const int r = 4 * g + vb + j;
-            if (r >= M || !((mask >> r) & 1u)) continue;
+            const bool on = st_lane && r < M && ((mask >> r) & 1u);  // uniform over the row of 16 lanes
             const float gv = as_bf16(gate[j]), uv = as_bf16(up[j]);
-            const float hv = as_bf16(silu(gv)) * uv;
-            p.h[(int64_t)R.slot_tab[u][r] * Nrows + n] = (uint16_t)f32_to_bf16(hv);
+            const uint32_t hb = f32_to_bf16(as_bf16(silu(gv)) * uv);
+            const int slot = on ? R.slot_tab[u][r] : 0;
+            if (on && n_in) p.h[(int64_t)slot * Nrows + n] = (uint16_t)hb;
+            if (p.h_sums) {
+                const float ts = qmm::detail::group_sum_c<16>(n_in ? bf16_to_f32(hb) : 0.f);
+                if (on && n16 == 0) p.h_sums[(int64_t)slot * T16 + tile] = ts;
+            }
         }
     };
 
@@ -319,7 +326,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
 // ---------------------------------------------------------------------------------------------------------------
 // down + combine. LDS (static): the S slot rows of h [S][K + 8] BF16 (code order), span sums [S][K / 128], a zero
 // block, the waves' partial sums [8][16 tokens][16 rows].
-template <int NB>
+template <int NB, bool SUMS>
 __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t hs[kHsElems];
     __shared__ __attribute__((aligned(16))) float hsum[kMaxSlots * kMaxSpansDn];
@@ -340,6 +347,17 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     int32_t my_id;
     float my_coef;
     my_id = p.ids[min(lane, S - 1)], my_coef = p.coef[min(lane, S - 1)];  // every wave: no branch around loads
+    constexpr int kSumLoads = SUMS ? (kMaxSlots * kMaxSpansDn + kThreads - 1) / kThreads : 0;
+    float4 tsum[kSumLoads > 0 ? kSumLoads : 1][2];  // SUMS: the 8 tile sums of (slot, span) i = b * kThreads + tid
+    if constexpr (SUMS) {
+        const int tiles = (int)(K / 16);
+#pragma unroll
+        for (int b = 0; b < kSumLoads; ++b) {
+            const int i = min(b * kThreads + tid, S * nspan - 1), r = i / nspan, sp = i - r * nspan;
+            const float4 *src = reinterpret_cast<const float4 *>(p.h_sums + (int64_t)r * tiles + sp * 8);
+            tsum[b][0] = src[0], tsum[b][1] = src[1];
+        }
+    }
     uint4 raw[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -398,17 +416,39 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    if constexpr (SUMS) {  // h in code order; span sums = the 8 tile sums in tile order
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int i = b * kThreads + tid;
-        if (i < n_items_x) {
-            const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
-            uint4 planes[1];
-            float sum;
-            qmm::detail::chunk_planes<4, 1, uint16_t>(raw[b], planes, sum);
-            *reinterpret_cast<uint4 *>(hs + r * ldh + (int64_t)c8 * 8) = planes[0];
-            sum = qmm::detail::group_sum_c<16>(sum);
-            if ((c8 & 15) == 0) hsum[r * nspan + (c8 >> 4)] = sum;
+        for (int b = 0; b < NB; ++b) {
+            const int i = b * kThreads + tid;
+            if (i < n_items_x) {
+                const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
+                const uint4 w = raw[b];
+                *reinterpret_cast<uint4 *>(hs + r * ldh + (int64_t)c8 * 8) =
+                    uint4{__builtin_amdgcn_perm(w.z, w.x, 0x05040100u), __builtin_amdgcn_perm(w.z, w.x, 0x07060302u),
+                          __builtin_amdgcn_perm(w.w, w.y, 0x05040100u), __builtin_amdgcn_perm(w.w, w.y, 0x07060302u)};
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kSumLoads; ++b) {
+            const int i = b * kThreads + tid;
+            if (i < S * nspan) {
+                const float4 a = tsum[b][0], c = tsum[b][1];
+                hsum[i] = ((((((a.x + a.y) + a.z) + a.w) + c.x) + c.y) + c.z) + c.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int i = b * kThreads + tid;
+            if (i < n_items_x) {
+                const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
+                uint4 planes[1];
+                float sum;
+                qmm::detail::chunk_planes<4, 1, uint16_t>(raw[b], planes, sum);
+                *reinterpret_cast<uint4 *>(hs + r * ldh + (int64_t)c8 * 8) = planes[0];
+                sum = qmm::detail::group_sum_c<16>(sum);
+                if ((c8 & 15) == 0) hsum[r * nspan + (c8 >> 4)] = sum;
+            }
         }
     }
     lds_barrier();  // the ring's weight loads stay in flight
@@ -513,9 +553,10 @@ hipError_t launch_down(const DownParams &p, hipStream_t stream) {
     const int n_items = p.M * p.A * (int)(p.K / 8);
     const int nb = (n_items + kThreads - 1) / kThreads;
     const dim3 grid((unsigned)((p.N + 15) / 16));
-    if (nb <= 4) down_kernel<4><<<grid, kThreads, 0, stream>>>(p);
-    else if (nb <= 8) down_kernel<8><<<grid, kThreads, 0, stream>>>(p);
-    else down_kernel<16><<<grid, kThreads, 0, stream>>>(p);
+    const bool sums = p.h_sums != nullptr;
+    if (nb <= 4) sums ? down_kernel<4, true><<<grid, kThreads, 0, stream>>>(p) : down_kernel<4, false><<<grid, kThreads, 0, stream>>>(p);
+    else if (nb <= 8) sums ? down_kernel<8, true><<<grid, kThreads, 0, stream>>>(p) : down_kernel<8, false><<<grid, kThreads, 0, stream>>>(p);
+    else sums ? down_kernel<16, true><<<grid, kThreads, 0, stream>>>(p) : down_kernel<16, false><<<grid, kThreads, 0, stream>>>(p);
     return hipGetLastError();
 }
 
@@ -567,8 +608,8 @@ int sx_moe_verify_supported(int64_t M, int64_t A, int64_t E, int64_t k, int64_t 
 
 int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
                           const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *w, int64_t Ew,
-                          int32_t *ids, float *coef, void *h, int act, uint32_t *router_err, uint32_t *expert_err,
-                          sx_stream stream) {
+                          int32_t *ids, float *coef, void *h, float *h_sums, int act, uint32_t *router_err,
+                          uint32_t *expert_err, sx_stream stream) {
     const char *fn = "sx_moe_verify_gate_up";
     const int64_t A = k + (shared_logit ? 1 : 0);
     SX_CHECK(x != nullptr && logits != nullptr && ids != nullptr && coef != nullptr && h != nullptr &&
@@ -579,26 +620,28 @@ int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t
     SX_CHECK(aligned(x, 16) && aligned(h, 2), fn, " x must be 16-byte aligned");
     const int64_t I = w->N / Ew / 2;
     SX_CHECK(apart(h, M * A * I * 2, x, M * w->K * 2), fn, " h overlaps x");
+    SX_CHECK(h_sums == nullptr || (aligned(h_sums, 16) && apart(h_sums, M * A * ((I + 15) / 16) * 4, h, M * A * I * 2)), fn,
+             " h_sums must be 16-byte aligned and apart from h");
     vf::GateUpParams p{};
     p.x = static_cast<const uint16_t *>(x), p.M = (int)M, p.A = (int)A, p.k = (int)k, p.E = (int)E, p.Ew = (int)Ew;
     p.logits = logits, p.ld = ld, p.shared_logit = shared_logit, p.shared_ld = shared_ld, p.shared_id = shared_id;
     p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = w->N / Ew, p.K = w->K;
-    p.ids = ids, p.coef = coef, p.h = static_cast<uint16_t *>(h), p.router_err = router_err, p.expert_err = expert_err;
+    p.ids = ids, p.coef = coef, p.h = static_cast<uint16_t *>(h), p.h_sums = h_sums, p.router_err = router_err, p.expert_err = expert_err;
     SX_HIP(vf::launch_gate_up(p, device_cus(), stream_of(stream)), fn);
     return SX_OK;
 }
 
-int sx_moe_verify_down(const void *h, int64_t M, int64_t A, const int32_t *ids, const float *coef, const sx_qview *w,
-                       int64_t Ew, void *y, int act, uint32_t *expert_err, sx_stream stream) {
+int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A, const int32_t *ids, const float *coef,
+                       const sx_qview *w, int64_t Ew, void *y, int act, uint32_t *expert_err, sx_stream stream) {
     const char *fn = "sx_moe_verify_down";
     SX_CHECK(h != nullptr && ids != nullptr && coef != nullptr && y != nullptr && expert_err != nullptr, fn,
              " null pointer");
     if (int rc = check_down(fn, M, A, Ew, w, act)) return rc;
-    SX_CHECK(aligned(h, 16), fn, " h must be 16-byte aligned");
+    SX_CHECK(aligned(h, 16) && aligned(h_sums, 16), fn, " h and h_sums must be 16-byte aligned");
     const int64_t N = w->N / Ew;
     SX_CHECK(apart(y, M * N * 2, h, M * A * w->K * 2), fn, " y overlaps h");
     vf::DownParams p{};
-    p.h = static_cast<const uint16_t *>(h), p.M = (int)M, p.A = (int)A, p.Ew = (int)Ew, p.ids = ids, p.coef = coef;
+    p.h = static_cast<const uint16_t *>(h), p.h_sums = h_sums, p.M = (int)M, p.A = (int)A, p.Ew = (int)Ew, p.ids = ids, p.coef = coef;
     p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = N, p.K = w->K, p.y = y, p.act = act;
     p.expert_err = expert_err;
     SX_HIP(vf::launch_down(p, stream_of(stream)), fn);

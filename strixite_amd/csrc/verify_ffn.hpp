@@ -25,11 +25,13 @@ struct GateUpParams {
     int32_t *ids;
     float *coef;
     uint16_t *h;        // BF16 [M * A, I]
+    float *h_sums;      // nullable: FP32 [M * A, ceil(I / 16)], each 16-feature run of an h row summed as stored
     uint32_t *router_err, *expert_err;
 };
 
 struct DownParams {
     const uint16_t *h;  // BF16 [M * A, K]
+    const float *h_sums;  // nullable: gate_up's 16-feature sums of h (else the span sums are taken from h here)
     int M, A, Ew;
     const int32_t *ids;
     const float *coef;

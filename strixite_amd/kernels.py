@@ -132,8 +132,9 @@ def verify_supported(M, A, E, k, Ew, gate_up, down, act=ACT_BF16):
 
 
 def verify_gate_up(x, logits, w, E, k, Ew=None, shared_logit=None, shared_id=0, ids=None, coef=None, h=None,
-                   router_err=None, expert_err=None, stream=None):
-    """moe_router + gather_swiglu in one launch at verify width: ids, coef [M, A], h [M, A, I]."""
+                   router_err=None, expert_err=None, h_sums=None, stream=None):
+    """moe_router + gather_swiglu in one launch at verify width: ids, coef [M, A], h [M, A, I]. h_sums (optional,
+    FP32 [M * A, ceil(I / 16)]) receives the 16-feature sums of h that verify_down can take."""
     M, ld = x.shape[0], logits.stride(0)
     Ew = E if Ew is None else Ew
     A = k + (shared_logit is not None)
@@ -146,19 +147,20 @@ def verify_gate_up(x, logits, w, E, k, Ew=None, shared_logit=None, shared_id=0, 
     expert_err = _err(dev) if expert_err is None else expert_err
     sld = 0 if shared_logit is None else shared_logit.stride(0)
     check(lib().sx_moe_verify_gate_up(_p(x), M, _p(logits), ld, E, k, _p(shared_logit), sld, shared_id, w.view(), Ew,
-                                      _p(ids), _p(coef), _p(h), act_of(x), _p(router_err), _p(expert_err),
-                                      _s(stream)))
+                                      _p(ids), _p(coef), _p(h), _p(h_sums), act_of(x), _p(router_err),
+                                      _p(expert_err), _s(stream)))
     return ids, coef, h, router_err, expert_err
 
 
-def verify_down(h, w, ids, coef, Ew, y=None, expert_err=None, stream=None):
-    """y[M, N] = sum_a coef[m, a] * (h[m, a] . W[ids[m, a]]) in one launch at verify width."""
+def verify_down(h, w, ids, coef, Ew, y=None, expert_err=None, h_sums=None, stream=None):
+    """y[M, N] = sum_a coef[m, a] * (h[m, a] . W[ids[m, a]]) in one launch at verify width (h_sums: verify_gate_up's
+    sums of this h, optional)."""
     M, A = ids.shape
     N = w.N // Ew
     y = torch.empty((M, N), dtype=h.dtype, device=h.device) if y is None else y
     expert_err = _err(h.device) if expert_err is None else expert_err
-    check(lib().sx_moe_verify_down(_p(h), M, A, _p(ids), _p(coef), w.view(), Ew, _p(y), act_of(h), _p(expert_err),
-                                   _s(stream)))
+    check(lib().sx_moe_verify_down(_p(h), _p(h_sums), M, A, _p(ids), _p(coef), w.view(), Ew, _p(y), act_of(h),
+                                   _p(expert_err), _s(stream)))
     return y, expert_err
 
 

@@ -30,6 +30,7 @@ class MoeVerifyLayer:
         self.expert_err = torch.zeros(4, dtype=torch.int32, device=dev)
         self.ws = torch.empty(kx.route_workspace_bytes(M, A, E) // 4, dtype=torch.int32, device=dev)
         self.h = torch.empty((M, A, self.I), dtype=act_dtype, device=dev)
+        self.h_sums = torch.empty((M * A, (self.I + 15) // 16), dtype=torch.float32, device=dev)
         self.partial = torch.empty((M * A, self.d), dtype=torch.float32, device=dev)
         self.y = torch.empty((M, self.d), dtype=act_dtype, device=dev)
         self.fused = fused and act_dtype == torch.bfloat16
@@ -44,9 +45,10 @@ class MoeVerifyLayer:
         kx.linear_f32w(x, self.Wr, y=self.logits[:M], stream=stream)
         if self._fused(M):
             kx.verify_gate_up(x, self.logits[:M], self.gate_up, self.E, self.k, ids=self.ids[:M], coef=self.coef[:M],
-                              h=self.h[:M], router_err=self.router_err, expert_err=self.expert_err, stream=stream)
+                              h=self.h[:M], router_err=self.router_err, expert_err=self.expert_err,
+                              h_sums=self.h_sums, stream=stream)
             kx.verify_down(self.h[:M], self.down, self.ids[:M], self.coef[:M], self.E, y=self.y[:M],
-                           expert_err=self.expert_err, stream=stream)
+                           expert_err=self.expert_err, h_sums=self.h_sums, stream=stream)
             return self.y[:M]
         if M * self.k <= 2048:  # top-k + grouping in one launch
             kx.router_group(self.logits[:M], self.E, self.k, ws=ws, ids=self.ids[:M], coef=self.coef[:M],

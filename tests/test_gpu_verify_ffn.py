@@ -27,23 +27,37 @@ def make(seed, Ew, I, d):
     return wgu, wdn, rng
 
 
-def run_fused(x, L, wgu, wdn, E, k, shared):
+def run_fused(x, L, wgu, wdn, E, k, shared, sums=True):
+    """gate_up then down; with `sums` gate_up also writes h_sums and down takes them (the layer's path), which is
+    checked here against h itself (each 16-feature run of a valid slot's row, summed in float64)."""
     import torch
     Ew = E + (1 if shared else 0)
     Wgu, Wdn = kx().QWeight.upload(wgu), kx().QWeight.upload(wdn)
     Ld = util.f32_dev(L)
     sl = Ld[:, E:] if shared else None
+    M, I = x.shape[0], wdn.K
+    A = k + (1 if shared else 0)
+    hs = torch.full((M * A, I // 16), float("nan"), dtype=torch.float32, device="cuda") if sums else None
     ids, coef, h, rerr, eerr = kx().verify_gate_up(util.bf16_dev(x), Ld, Wgu, E, k, Ew=Ew, shared_logit=sl,
-                                                   shared_id=E)
-    y, _ = kx().verify_down(h, Wdn, ids, coef, Ew, expert_err=eerr)
+                                                   shared_id=E, h_sums=hs)
+    y, _ = kx().verify_down(h, Wdn, ids, coef, Ew, expert_err=eerr, h_sums=hs)
     sync()
-    return (ids.cpu().numpy(), coef.cpu().numpy(), util.host_bits(h), util.host_bits(y),
+    hb = util.host_bits(h)
+    if sums:
+        hf = util.as_f32(hb).reshape(M * A, I // 16, 16).astype(np.float64)
+        ref = hf.sum(-1)
+        got = hs.cpu().numpy().astype(np.float64)
+        ok = ~np.isnan(ref).any(-1)  # the valid slots (NaN h rows: invalid, their sums unwritten)
+        bound = 1e-6 * np.abs(hf).sum(-1)
+        assert (np.abs(got[ok] - ref[ok]) <= bound[ok]).all(), "h_sums differ from the sums of h"
+    return (ids.cpu().numpy(), coef.cpu().numpy(), hb, util.host_bits(y),
             rerr.cpu().numpy()[:3].view(np.uint32), eerr.cpu().numpy()[:3].view(np.uint32))
 
 
+@pytest.mark.parametrize("sums", [True, False])
 @pytest.mark.parametrize("M,E,k,d,shared", [(6, 64, 10, 512, False), (1, 16, 4, 1024, False), (16, 40, 3, 512, True),
                                             (5, 300, 8, 2048, True), (4, 1000, 16, 512, False)])
-def test_verify_ffn_matches_oracle(M, E, k, d, shared):
+def test_verify_ffn_matches_oracle(M, E, k, d, shared, sums):
     I = 1024
     Ew = E + (1 if shared else 0)
     wgu, wdn, rng = make(M * 7 + E, Ew, I, d)
@@ -51,7 +65,7 @@ def test_verify_ffn_matches_oracle(M, E, k, d, shared):
     L = (rng.standard_normal((M, Ew)) * 1.3).astype(np.float32)
     if E >= 8:
         L[0, [2, 5]] = 4.0  # a tie: lower index first
-    ids, coef, h, y, rerr, eerr = run_fused(x, L, wgu, wdn, E, k, shared)
+    ids, coef, h, y, rerr, eerr = run_fused(x, L, wgu, wdn, E, k, shared, sums)
     if shared:
         r_ids, r_coef, r_err = orc.moe_router(L, E, k, shared=L[:, E].copy(), shared_ld=1, shared_id=E)
     else:
