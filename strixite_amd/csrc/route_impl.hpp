@@ -117,36 +117,79 @@ __device__ void route_values(float (&v)[NV], int E, int k, bool has_shared, floa
         }
         return;
     }
-    // Padding past E never wins: its key (0) is below every finite logit's. Each lane sorts its keys once; a round
-    // takes the wave maximum of the lane heads and the lane that owned it pops its head.
-    uint64_t keys[NV];
+    // Padding past E never wins: its value key (0) is below every finite logit's.
+    uint32_t hv[NV];  // value keys (the monotone bits)
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int e = lane + 64 * j;
-        keys[j] = e < E ? route_key(v[j], e) : 0;
+        hv[j] = e < E ? (uint32_t)(route_key(v[j], e) >> 32) : 0u;
     }
-    sort_desc<NV>(keys);
-    // A round: the wave maximum of the lane heads' value keys (32-bit DPP); a tie between lanes goes to the lower
-    // expert index (a second reduction, only then); the lane that owned the winner pops its head.
-    uint32_t hv[NV], hx[NV];  // value key (the monotone bits), expert index; padding: 0, 0xFFFFFFFF
-#pragma unroll
-    for (int j = 0; j < NV; ++j) hv[j] = (uint32_t)(keys[j] >> 32), hx[j] = 0xFFFFFFFFu - (uint32_t)keys[j];
     float my_v = -INFINITY, top = 0.f;
     int my_i = -1;
-    for (int r = 0; r < k; ++r) {
-        const uint32_t best = wave_max_u32(hv[0]);  // uniform
-        const bool cand = hv[0] == best;
-        const uint64_t cands = __ballot(cand);
-        const uint32_t bi = __popcll(cands) == 1 ? (uint32_t)__builtin_amdgcn_readlane((int)hx[0], __builtin_ctzll(cands))
-                                                 : wave_min_u32(cand ? hx[0] : 0xFFFFFFFFu);
-        const float bv = key_value((uint64_t)best << 32);
-        if (r == 0) top = bv;
-        if (lane == r) my_v = bv, my_i = (int)bi;
-        const bool pop = cand && hx[0] == bi;  // one lane: a lane's indices are distinct
+    // T = the k-th largest of the 64 lane maxima (counted with multiplicity), bit by bit: k lanes hold an element
+    // >= T, so every one of the top k is >= T. The candidates (>= T; usually a few more than k) go to lanes
+    // 0 .. C-1, each takes its rank among them by (value desc, index asc), and a permute puts pick r in lane r.
+    uint32_t lm = hv[0];
 #pragma unroll
-        for (int j = 0; j + 1 < NV; ++j) hv[j] = pop ? hv[j + 1] : hv[j], hx[j] = pop ? hx[j + 1] : hx[j];
-        hv[NV - 1] = pop ? 0u : hv[NV - 1];
-        hx[NV - 1] = pop ? 0xFFFFFFFFu : hx[NV - 1];
+    for (int j = 1; j < NV; ++j) lm = max(lm, hv[j]);
+    uint32_t T = 0u;
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t t = T | (1u << b);
+        if (__popcll(__ballot(lm >= t)) >= k) T = t;  // uniform
+    }
+    uint32_t cv = 0u, cx = 0xFFFFFFFFu;  // this lane's candidate: value key, index
+    int C = 0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        for (uint64_t bal = __ballot(hv[j] >= T); bal; bal &= bal - 1, ++C) {
+            const int s = __builtin_ctzll(bal);
+            if (C < 64) {
+                const uint32_t val = (uint32_t)__builtin_amdgcn_readlane((int)hv[j], s);
+                if (lane == C) cv = val, cx = (uint32_t)(64 * j + s);
+            }
+        }
+    }
+    if (C <= 64) {
+        int rank = 0;
+        for (int c = 0; c < C; ++c) {
+            const uint32_t ov = (uint32_t)__builtin_amdgcn_readlane((int)cv, c);
+            const uint32_t ox = (uint32_t)__builtin_amdgcn_readlane((int)cx, c);
+            rank += (ov > cv || (ov == cv && ox < cx)) ? 1 : 0;
+        }
+        if (lane >= C) rank = lane;  // ranks 0 .. C-1 of the candidates plus the other lanes: a permutation
+        const uint32_t pv = (uint32_t)__builtin_amdgcn_ds_permute(rank * 4, (int)cv);
+        const uint32_t px = (uint32_t)__builtin_amdgcn_ds_permute(rank * 4, (int)cx);
+        top = key_value((uint64_t)__builtin_amdgcn_readfirstlane(pv) << 32);
+        if (lane < k) my_v = key_value((uint64_t)pv << 32), my_i = (int)px;
+    } else {
+        // Many ties at the threshold: k rounds of the wave maximum over each lane's sorted keys, the lane owning the
+        // winner popping its head (a tie between lanes goes to the lower index: a second reduction, only then).
+        uint64_t keys[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int e = lane + 64 * j;
+            keys[j] = e < E ? route_key(v[j], e) : 0;
+        }
+        sort_desc<NV>(keys);
+        uint32_t hx[NV];  // expert index; padding: 0xFFFFFFFF
+#pragma unroll
+        for (int j = 0; j < NV; ++j) hv[j] = (uint32_t)(keys[j] >> 32), hx[j] = 0xFFFFFFFFu - (uint32_t)keys[j];
+        for (int r = 0; r < k; ++r) {
+            const uint32_t best = wave_max_u32(hv[0]);  // uniform
+            const bool cand = hv[0] == best;
+            const uint64_t cands = __ballot(cand);
+            const uint32_t bi = __popcll(cands) == 1
+                                    ? (uint32_t)__builtin_amdgcn_readlane((int)hx[0], __builtin_ctzll(cands))
+                                    : wave_min_u32(cand ? hx[0] : 0xFFFFFFFFu);
+            const float bv = key_value((uint64_t)best << 32);
+            if (r == 0) top = bv;
+            if (lane == r) my_v = bv, my_i = (int)bi;
+            const bool pop = cand && hx[0] == bi;  // one lane: a lane's indices are distinct
+#pragma unroll
+            for (int j = 0; j + 1 < NV; ++j) hv[j] = pop ? hv[j + 1] : hv[j], hx[j] = pop ? hx[j + 1] : hx[j];
+            hv[NV - 1] = pop ? 0u : hv[NV - 1];
+            hx[NV - 1] = pop ? 0xFFFFFFFFu : hx[NV - 1];
+        }
     }
     const float ex = lane < k ? expf(my_v - top) : 0.f;
     const float sum = wave_sum_f32(ex);
@@ -161,8 +204,9 @@ __device__ void route_values(float (&v)[NV], int E, int k, bool has_shared, floa
 }
 
 // Token m's routing by one wave: the E logits (load(e) -> float) stay in registers, lane l holding experts
-// l, l + 64, ...; k rounds of a wave-wide key maximum, only the lane whose expert was picked rescanning its
-// registers; then the softmax over the k picks (coef = exp(l - l_max) / sum). A non-finite logit (or shared gate)
+// l, l + 64, ...; a threshold below which no top-k value lies (bit-by-bit search over the lane maxima), the few
+// candidates above it ranked against each other (k rounds of a wave-wide maximum instead when more than 64 values
+// reach the threshold); then the softmax over the k picks (coef = exp(l - l_max) / sum). A non-finite logit (or shared gate)
 // fails the token: ids -1, coefficients NaN, err = {1, m, expert} (first wins). With has_shared, slot k is the
 // shared expert with coefficient sigmoid(sl). lds_row (may be null) receives the ids too.
 template <int NV, typename Load>

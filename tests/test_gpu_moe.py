@@ -31,6 +31,8 @@ def test_router_ids_bit_exact(E, k):
         L[4, :] = 0.5                         # everything tied
         L[5, :] = -0.0
         L[5, E - 1] = 0.0                     # -0 ties +0
+        L[6, :] = rng.integers(0, 40, E)      # ties straddling the k-th value (a few dozen candidates)
+        L[7, :] = np.round(L[7] * 2) / 2      # coarse levels
     ids, coef, err = kx().moe_router(util.f32_dev(L), E, k)
     sync()
     ref_ids, ref_coef, ref_err = orc.moe_router(L, E, k)
