@@ -54,6 +54,18 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// Inclusive prefix sum over the wave's lanes: row_shr 1, 2, 4, 8 scan each row of 16 (a lane with no source
+// adds `old` = 0), then row_bcast:15 and row_bcast:31 carry the row totals into the rows after them.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+    v += dpp_u32<0x111>(0u, v);
+    v += dpp_u32<0x112>(0u, v);
+    v += dpp_u32<0x114>(0u, v);
+    v += dpp_u32<0x118>(0u, v);
+    v += dpp_u32<0x142, 0xA>(0u, v);
+    v += dpp_u32<0x143, 0xC>(0u, v);
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum_f32(float x) {
     auto add = [](float a, uint32_t b) { return a + __uint_as_float(b); };
     x = add(x, dpp_u32<0xB1>(0u, __float_as_uint(x)));

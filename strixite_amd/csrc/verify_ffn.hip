@@ -49,18 +49,18 @@ struct Routes {                // one block's copy of the routing (LDS)
 // The distinct experts of the slots in id order with their token masks. bad_slots marks ids outside [0, Ew) and
 // repeats of an id within a token (the routers never produce one; such a slot is treated as invalid: the later
 // slot of the two). Wave 0 alone does it, from `id` = its lane's slot id (lane < S): the LDS operations of one wave
-// take effect in program order, so no barrier is needed until the closing one. Experts go by passes of 64 (pass j:
-// experts 64 j + lane), a ballot and its lane count placing each pass's units after the previous pass's.
-// emask: LDS [kMaxExperts]. Ends with an LDS-only block barrier.
+// take effect in program order, so no barrier is needed until the closing one. Lane t owns experts kPer t ..
+// kPer t + kPer - 1: their token masks in four 16-byte reads, a wave prefix sum of the counts placing its units.
+// emask: LDS [kMaxExperts], 16-byte aligned. Ends with an LDS-only block barrier.
 __device__ void build_units(Routes &R, uint32_t *emask, int32_t id, int S, int A, int Ew) {
-    constexpr int kPass = kMaxExperts / 64;
+    constexpr int kPer = kMaxExperts / 64, kQuads = kPer / 4;
+    static_assert(kPer % 4 == 0, "experts a lane: whole 16-byte words");
+    static_assert(kMaxSlots * kMaxTokens == 64 * 16, "slot_tab: one 16-byte row a lane");
     const int t = threadIdx.x;
     if (t < 64) {
-        const int passes = (Ew + 63) >> 6;
+        uint4 *mine = reinterpret_cast<uint4 *>(emask) + t * kQuads;
 #pragma unroll
-        for (int j = 0; j < kPass; ++j)
-            if (j < passes) emask[64 * j + t] = 0u;
-        static_assert(kMaxSlots * kMaxTokens == 64 * 16, "slot_tab: one 16-byte row a lane");
+        for (int q = 0; q < kQuads; ++q) mine[q] = uint4{0u, 0u, 0u, 0u};
         reinterpret_cast<int4 *>(&R.slot_tab[0][0])[t] = make_int4(-1, -1, -1, -1);
         const bool in = t < S;
         bool bad = in && !(id >= 0 && id < Ew);
@@ -74,20 +74,22 @@ __device__ void build_units(Routes &R, uint32_t *emask, int32_t id, int S, int A
             }
         }
         const uint64_t bad_mask = __ballot(bad);
-        uint32_t mk[kPass];
+        uint32_t mk[kPer];
 #pragma unroll
-        for (int j = 0; j < kPass; ++j) mk[j] = j < passes ? emask[64 * j + t] : 0u;
-        int base = 0;
-#pragma unroll
-        for (int j = 0; j < kPass; ++j) {
-            if (j >= passes) break;
-            const uint64_t bal = __ballot(mk[j] != 0u);
-            const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-            if (mk[j]) R.u_exp[pos] = 64 * j + t, R.u_mask[pos] = mk[j], emask[64 * j + t] = (uint32_t)pos;
-            base += __popcll(bal);
+        for (int q = 0; q < kQuads; ++q) {
+            const uint4 w = mine[q];
+            mk[4 * q] = w.x, mk[4 * q + 1] = w.y, mk[4 * q + 2] = w.z, mk[4 * q + 3] = w.w;
         }
-        if (t == 0) R.U = base, R.bad_slots = bad_mask;
+        uint32_t c = 0u;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) c += mk[j] != 0u;
+        const uint32_t incl = routing::wave_incl_scan_u32(c);
+        int pos = (int)(incl - c);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j)
+            if (mk[j]) R.u_exp[pos] = kPer * t + j, R.u_mask[pos] = mk[j], emask[kPer * t + j] = (uint32_t)pos++;
+        if (t == 63) R.U = (int)incl;
+        if (t == 0) R.bad_slots = bad_mask;
         if (in && !bad) R.slot_tab[emask[id]][t / A] = (int8_t)t;
     }
     lds_barrier();  // the loads in flight (activations, weights) keep going
@@ -106,7 +108,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
     constexpr int P = kWaves / Q;  // items a round
     __shared__ __attribute__((aligned(16))) float red[2][kWaves][2][4][64];  // [round & 1][wave][gate, up][v][lane]
     __shared__ Routes R;
-    __shared__ uint32_t emask[kMaxExperts];
+    __shared__ __attribute__((aligned(16))) uint32_t emask[kMaxExperts];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -333,7 +335,7 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t zero_block[kZeroBytes / 2];
     __shared__ __attribute__((aligned(16))) float red[kWaves][16][16];
     __shared__ Routes R;
-    __shared__ uint32_t emask[kMaxExperts];
+    __shared__ __attribute__((aligned(16))) uint32_t emask[kMaxExperts];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
