@@ -15,9 +15,10 @@
 //     wave in expert order, then across the waves in LDS in a fixed order: deterministic, no FP32 partials in
 //     memory and no separate combine.
 //
-// Both stream their weight tiles with the scheme of qmm_impl.hpp's fast path: a lane loads 16 code bytes a step
-// (16 rows x one 64-byte span a wave), groups of 8 steps with their scale / min windows, 2 groups in flight, and
-// v_mfma_f32_16x16x32_bf16 on BF16 (128 + code) against the LDS-staged activations:
+// Both stream their weight tiles like qmm_impl.hpp's fast path: a lane loads 16 code bytes a step (16 rows x one
+// 64-byte span a wave) with the spans' scale / min windows, one round of loads in flight a wave (gate_up: 8 loads,
+// down: 4; deeper rings measured slower: more requests in flight a CU lowered the HBM rate), and
+// v_mfma_f32_16x16x32_bf16 on BF16 (128 + code) against the activations:
 //   sum_k x * (code * s + m) = s * D + (m - 128 s) * sum_span x.
 #include "qmm_impl.hpp"
 #include "route_impl.hpp"
@@ -31,9 +32,9 @@ using qmm::detail::f32x4;
 using qmm::detail::kPrefetch;
 
 constexpr int kThreads = 512, kWaves = 8;
-constexpr int kRing = 2;  // groups of 8 loads in flight a wave (16 KB a wave, 128 KB a CU; 3 measured slower)
+constexpr int kRing = 1;  // rounds of 8 loads in flight a wave (8 KB a wave, 64 KB a CU: measured faster than 2 or 3)
 constexpr int kSpan = 128, kSpanBytes = 64;
-constexpr int kSpansDn = 4, kRingDn = 4;  // down: an item is 4 spans of a unit (4 loads a wave), 4 items in flight
+constexpr int kSpansDn = 4, kRingDn = 1;  // down: an item is 4 spans of a unit (4 loads a wave), one item in flight (2, 4 measured slower)
 constexpr int kZeroBytes = qmm::detail::kZeroBytes;
 
 struct Routes {                // one block's copy of the routing (LDS)
@@ -98,7 +99,7 @@ __device__ void build_units(Routes &R, uint32_t *emask, int32_t id, int S, int A
 // ---------------------------------------------------------------------------------------------------------------
 // gate_up + SwiGLU. A block takes an equal run of the (expert, 16-feature tile) items (to within one item of every
 // other block); its 8 waves split K Q ways (Q = K / 512: four spans a wave) and take 8 / Q items a round, so every
-// wave of the grid streams the same bytes: 8 loads a round (4 spans x gate, up), 2 rounds in flight. The Q partial
+// wave of the grid streams the same bytes: 8 loads a round (4 spans x gate, up), one round in flight. The Q partial
 // tiles of an item are summed in LDS after a barrier (Q > 1), in K order, and the item's SwiGLU rows are stored by
 // the Q waves that made them, a quarter-tile or less each. A wave's four spans of the M activation rows sit in its
 // registers as MFMA A operands (code order) for the whole kernel, with their span sums. LDS (static): the partial
@@ -318,10 +319,10 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
     // Runs of kRing rounds, all issuing their loads (an odd count ends with a phantom round that re-loads the last
     // one and stops after its MFMAs): a consume whose loads were conditional would merge two versions of the ring
     // registers, and the copies at such a merge wait for every outstanding load.
-    for (int gr = 0; gr < groups; gr += kRing) {
-        consume(gr, std::integral_constant<int, 0>{});
-        consume(gr + 1, std::integral_constant<int, 1>{});
-    }
+    for (int gr = 0; gr < groups; gr += kRing)
+        [&]<int... RS>(std::integer_sequence<int, RS...>) {
+            (consume(gr + RS, std::integral_constant<int, RS>{}), ...);
+        }(std::make_integer_sequence<int, kRing>{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave exits
 }
 
@@ -502,12 +503,10 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     // Runs of kRingDn items, all issuing their loads (a count short of a multiple ends with phantom items that
     // re-load the last one and stop after their MFMAs): a consume whose loads were conditional would merge two
     // versions of the ring registers, and the copies at such a merge wait for every outstanding load.
-    for (int gr = 0; gr < groups; gr += kRingDn) {
-        consume(gr, std::integral_constant<int, 0>{});
-        consume(gr + 1, std::integral_constant<int, 1>{});
-        consume(gr + 2, std::integral_constant<int, 2>{});
-        consume(gr + 3, std::integral_constant<int, 3>{});
-    }
+    for (int gr = 0; gr < groups; gr += kRingDn)
+        [&]<int... RS>(std::integer_sequence<int, RS...>) {
+            (consume(gr + RS, std::integral_constant<int, RS>{}), ...);
+        }(std::make_integer_sequence<int, kRingDn>{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom items' loads land before the wave exits
 
     // the waves' sums in wave order; tokens with an invalid slot get NaN rows (the combine's rule)
