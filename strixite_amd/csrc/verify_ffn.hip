@@ -32,6 +32,7 @@ using qmm::detail::f32x4;
 using qmm::detail::kPrefetch;
 
 constexpr int kThreads = 512, kWaves = 8;
+constexpr int kLag = 2;  // a slot's reload goes out two slots after its unpack (fewer loads in flight: measured faster)
 constexpr int kRing = 1;  // rounds of 8 loads in flight a wave (8 KB a wave, 64 KB a CU: measured faster than 2 or 3)
 constexpr int kSpan = 128, kSpanBytes = 64;
 constexpr int kSpansDn = 4, kRingDn = 1;  // down: an item is 4 spans of a unit (4 loads a wave), one item in flight (2, 4 measured slower)
@@ -280,7 +281,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
                             // value still live there would make the loop rotate the ring behind a full wait)
 #pragma unroll
             for (int t = 0; t < 4; ++t) bop[t] = qmm::detail::codes_b<4>(ring[RS][s], t);
-            issue_slot(ring[RS], s);
+            if (s >= kLag) issue_slot(ring[RS], s - kLag);
             f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[so][t], bop[t], D, 0, 0, 0);
@@ -291,6 +292,8 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[w][v] = fmaf(s_, D[v], fmaf(cm, xv[so][v], acc[w][v]));
         }
+#pragma unroll
+        for (int s = kPrefetch - kLag; s < kPrefetch; ++s) issue_slot(ring[RS], s);
         if (gr >= groups) return;  // the phantom round
         const int item = b0 + gr * P + ip;
         if constexpr (Q == 1) {
