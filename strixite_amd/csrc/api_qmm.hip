@@ -81,7 +81,7 @@ int linear(const char *fn, int bits, const void *x, const sx_qview *w, void *y, 
              " with input ", act, " unsupported (same dtype, or BF16 -> F32)");
     SX_CHECK(apart(x, M * w->K * act_bytes(act), y, M * w->N * act_bytes(out_act)), fn, " output y [", y, ", +",
              M * w->N * act_bytes(out_act), " B) overlaps input x [", x, ", +", M * w->K * act_bytes(act), " B)");
-    if (dks::eligible(bits, w->G, w->N, w->K, M, act, out_act, device_cus())) {  // few tiles: K split over the waves
+    if (dks::eligible(bits, w->G, w->N, w->K, M, act, out_act, device_cus())) {  // decode width: K split over a block
         dks::Params d{};
         d.x = x, d.q = w->q, d.scale = w->scale, d.minv = w->minv, d.y = y, d.M = (int)M, d.N = w->N, d.K = w->K;
         SX_HIP(dks::launch(bits, act, out_act, d, device_cus(), stream_of(stream)), fn);

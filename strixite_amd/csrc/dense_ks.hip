@@ -1,10 +1,10 @@
 // Dense dequantizing GEMV at decode / verify width (M <= 16 activation rows): y[M, N] = x[M, K] . deq(W)^T for q4
 // (G = 128) and q8 (G = 64), one quantization group a 16-byte-a-lane span (kernels/linear_q4.hpp:26-30,
-// kernels/linear_q8.hpp:13-14). Beside qmm's dense mode (a wave a 16-row tile over the whole K) for the shapes where
-// the rows alone do not fill the chip: configs 1-2 have 256-768 tiles of 32-64 spans, a round trip or more of
-// latency a tile on a few waves a CU. Here every block takes an equal run of the 16-row tiles (to within one
-// tile), and its 8 waves split K Q ways (Q = min(8, spans / 4)) and work on 8 / Q tiles at a time, so every wave of
-// the grid issues the same loads: SPW spans a round (4 or 8 loads of 1 KB), two rounds in flight. The activation
+// kernels/linear_q8.hpp:13-14), for the served shapes (4-64 spans a row) in place of qmm's dense mode (a wave a
+// 16-row tile over the whole K, many tiles a CU in flight at once). A block a CU takes an equal run of the 16-row
+// tiles (to within one tile), and its 8 waves split K Q ways (Q = min(8, spans / 4)) and work on 8 / Q tiles at a
+// time, so every wave of the grid issues the same loads: SPW spans a round (4 or 8 loads of 1 KB), one round in
+// flight, and a CU reads one tile's rows at a time (measured faster than more tiles in flight a CU). The activation
 // rows sit in LDS once per block (BF16 x: one plane; FP32 x: three exact BF16 planes) in the B operand's code order
 // with their span sums; each span folds as acc += s * D + (m - off * s) * sum x with D from
 // v_mfma_f32_16x16x32_bf16 on (off + code). The Q partial 16 x 16 tiles of a tile meet in LDS after a barrier (Q > 1),
@@ -22,6 +22,10 @@ using qmm::detail::f32x4;
 
 constexpr int kThreads = 512, kWaves = 8;
 constexpr int kSpanBytes = 64;  // a row's span: 16 bytes a lane, 4 lanes
+// One round of loads in flight a wave, and a slot's reload going out kLag slots after its unpack (2 of 4, 6 of 8):
+// fewer requests in flight a CU measured faster (config 1 12.0 -> 8.6 us, the q8 LM head 139 -> 126 us).
+constexpr int kRingKs = 1;
+template <int SPW> constexpr int kLagKs = SPW == 8 ? 6 : 2;
 
 // The BF16 word of span s in a window of 4 (uint2) or 8 (uint4) scales / mins.
 __device__ __forceinline__ uint32_t win_word(const uint2 &w, int s) { return s < 2 ? w.x : w.y; }
@@ -52,8 +56,8 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     // valid tile and stores nothing); the round's scales / mins as one window of SPW BF16 a row
     using Win = std::conditional_t<SPW == 4, uint2, uint4>;
     const int64_t rowbytes = K * BITS / 8, ngroups = nspan;
-    uint4 ring[2][SPW];
-    Win sw_n[2], mw_n[2];
+    uint4 ring[kRingKs][SPW];
+    Win sw_n[kRingKs], mw_n[kRingKs];
     int ii = 0;
     const uint8_t *iq = p.q;
     const uint16_t *is_ = p.scale, *im = p.minv;
@@ -112,7 +116,7 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
         __builtin_amdgcn_sched_barrier(0);
         iplace();
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < kRingKs; ++r) {
             if (r > 0) advance_issue();  // unconditional (iplace clamps): a branch would copy the ring behind a full wait
             issue_window(sw_n[r], mw_n[r]);
 #pragma unroll
@@ -146,7 +150,7 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     auto consume = [&](int gr, auto slot_tag) __attribute__((always_inline)) {
         constexpr int RS = decltype(slot_tag)::value;
         const Win sw = sw_n[RS], mw = mw_n[RS];
-        if (gr + 2 < groups) advance_issue();
+        if (gr + kRingKs < groups) advance_issue();
         issue_window(sw_n[RS], mw_n[RS]);
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -154,7 +158,7 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
             bf16x8 bop[F::kMfmas];  // unpacked before the reload is issued: the slot's register is then free for it
 #pragma unroll
             for (int t = 0; t < F::kMfmas; ++t) bop[t] = qmm::detail::codes_b<BITS>(ring[RS][s], t);
-            issue_slot(ring[RS], s);
+            if (s >= kLagKs<SPW>) issue_slot(ring[RS], s - kLagKs<SPW>);
             f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int pl = 0; pl < NPL; ++pl)
@@ -174,6 +178,8 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
             acc[2] = fmaf(s_, D[2], fmaf(cm, xv.z, acc[2]));
             acc[3] = fmaf(s_, D[3], fmaf(cm, xv.w, acc[3]));
         }
+#pragma unroll
+        for (int s = SPW - kLagKs<SPW>; s < SPW; ++s) issue_slot(ring[RS], s);
         if (gr >= groups) return;  // the phantom round
         const int tile = b0 + gr * P + ip;
         if (Q == 1) {
@@ -199,10 +205,10 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     // Runs of two rounds, all issuing their loads (an odd count ends with a phantom round that re-loads the last one
     // and stops after its MFMAs): a consume whose loads were conditional would merge two versions of the ring
     // registers, and the copies at such a merge wait for every outstanding load.
-    for (int gr = 0; gr < groups; gr += 2) {
-        consume(gr, std::integral_constant<int, 0>{});
-        consume(gr + 1, std::integral_constant<int, 1>{});
-    }
+    for (int gr = 0; gr < groups; gr += kRingKs)
+        [&]<int... RS>(std::integer_sequence<int, RS...>) {
+            (consume(gr + RS, std::integral_constant<int, RS>{}), ...);
+        }(std::make_integer_sequence<int, kRingKs>{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave exits
 }
 
@@ -231,12 +237,13 @@ size_t lds_bytes(int act, int64_t M, int64_t K, int bits) {
 }
 
 bool eligible(int bits, int64_t G, int64_t N, int64_t K, int64_t M, int act, int out_act, int cus) {
+    (void)N, (void)cus;  // any number of tiles: a block takes a run of them
     if (!((bits == 4 && G == 128) || (bits == 8 && G == 64))) return false;
     const int64_t span = bits == 4 ? 128 : 64;
     if (K % span != 0) return false;
     const int64_t nspan = K / span;
     if (!(nspan == 4 || nspan == 8 || nspan == 16 || nspan == 32 || nspan == 64)) return false;
-    if (M < 1 || M > 16 || (N + 15) / 16 > cus) return false;
+    if (M < 1 || M > 16) return false;
     if (!((act == SX_ACT_BF16 && (out_act == SX_ACT_BF16 || out_act == SX_ACT_F32)) ||
           (act == SX_ACT_F32 && out_act == SX_ACT_F32)))
         return false;

@@ -12,7 +12,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPrefetch = 8;  // steps (16-byte loads a lane) a group
-constexpr int kRing = 2;      // groups in flight a wave (fast path)
+constexpr int kRing = 1;      // groups in flight a wave (fast path)
 constexpr int kStageLoads = 8;  // activation chunk loads in flight a thread while staging
 constexpr int kZeroBytes = 2048;  // zero A operand for a group of idle-lane reads (8 q4 spans of BF16)
 
@@ -538,7 +538,7 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(Params p) {
         // The ring slot of group gr is gr % kRing: the loop takes kRing groups a trip so that slots are constants.
         for (int gr = 0; gr < groups; gr += kRing) {
             consume(gr, std::integral_constant<int, 0>{});
-            if (gr + 1 < groups) consume(gr + 1, std::integral_constant<int, 1>{});
+            if constexpr (kRing > 1) if (gr + 1 < groups) consume(gr + 1, std::integral_constant<int, (kRing > 1 ? 1 : 0)>{});
             if constexpr (kRing > 2) if (gr + 2 < groups) consume(gr + 2, std::integral_constant<int, (kRing > 2 ? 2 : 0)>{});
             if constexpr (kRing > 3) if (gr + 3 < groups) consume(gr + 3, std::integral_constant<int, (kRing > 3 ? 3 : 0)>{});
         }
