@@ -35,6 +35,7 @@ constexpr int kThreads = 512, kWaves = 8;
 constexpr int kLag = 2;  // a slot's reload goes out two slots after its unpack (fewer loads in flight: measured faster)
 constexpr int kRing = 1;  // rounds of 8 loads in flight a wave (8 KB a wave, 64 KB a CU: measured faster than 2 or 3)
 constexpr int kSpan = 128, kSpanBytes = 64;
+constexpr int kLagDn = 2;  // down: a slot's reload two slots after its unpack
 constexpr int kSpansDn = 4, kRingDn = 1;  // down: an item is 4 spans of a unit (4 loads a wave), one item in flight (2, 4 measured slower)
 constexpr int kZeroBytes = qmm::detail::kZeroBytes;
 
@@ -481,7 +482,7 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
                             // value still live there would make the loop rotate the ring behind a full wait)
 #pragma unroll
             for (int t = 0; t < 4; ++t) bop[t] = qmm::detail::codes_b<4>(ring[RS][s], t);
-            issue_slot(ring[RS], s);
+            if (s >= kLagDn) issue_slot(ring[RS], s - kLagDn);
             f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -498,6 +499,8 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
                 acc[v] = fmaf(s_, D[v], fmaf(cm, xv, acc[v]));
             }
         }
+#pragma unroll
+        for (int s = SPG - kLagDn; s < SPG; ++s) issue_slot(ring[RS], s);
         if (gr >= groups) return;  // a phantom item
 #pragma unroll
         for (int v = 0; v < 4; ++v)
