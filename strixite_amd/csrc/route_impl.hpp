@@ -145,32 +145,37 @@ __device__ void route_values(float (&v)[NV], int E, int k, bool has_shared, floa
 #pragma unroll
     for (int j = 1; j < NV; ++j) lm = max(lm, hv[j]);
     uint32_t T = 0u;
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t t = T | (1u << b);
-        if (__popcll(__ballot(lm >= t)) >= k) T = t;  // uniform
+    for (int b = 30; b >= 0; b -= 2) {  // two bits a step: three independent counts
+        const uint32_t t1 = T | (1u << b), t2 = T | (2u << b), t3 = T | (3u << b);
+        const int c1 = __popcll(__ballot(lm >= t1)), c2 = __popcll(__ballot(lm >= t2)), c3 = __popcll(__ballot(lm >= t3));
+        T = c3 >= k ? t3 : c2 >= k ? t2 : c1 >= k ? t1 : T;  // uniform
     }
-    uint32_t cv = 0u, cx = 0xFFFFFFFFu;  // this lane's candidate: value key, index
+    // the candidates' keys (value desc, index asc as one unsigned order) into this wave's LDS row, in (j, lane) order
+    __shared__ uint64_t route_cand[16][64];
+    uint64_t *cand = route_cand[(threadIdx.x >> 6) & 15];
     int C = 0;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        for (uint64_t bal = __ballot(hv[j] >= T); bal; bal &= bal - 1, ++C) {
-            const int s = __builtin_ctzll(bal);
-            if (C < 64) {
-                const uint32_t val = (uint32_t)__builtin_amdgcn_readlane((int)hv[j], s);
-                if (lane == C) cv = val, cx = (uint32_t)(64 * j + s);
-            }
-        }
+        const bool in = hv[j] >= T;
+        const uint64_t bal = __ballot(in);
+        const int pos = C + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (in && pos < 64) cand[pos] = ((uint64_t)hv[j] << 32) | (0xFFFFFFFFu - (uint32_t)(lane + 64 * j));
+        C += __popcll(bal);
     }
     if (C <= 64) {
+        // one wave's LDS accesses take effect in program order: the writes above precede these reads
+        const uint64_t mine = lane < C ? cand[lane] : 0ull;
         int rank = 0;
-        for (int c = 0; c < C; ++c) {
-            const uint32_t ov = (uint32_t)__builtin_amdgcn_readlane((int)cv, c);
-            const uint32_t ox = (uint32_t)__builtin_amdgcn_readlane((int)cx, c);
-            rank += (ov > cv || (ov == cv && ox < cx)) ? 1 : 0;
+        for (int c = 0; c < C; c += 4) {  // uniform
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint64_t o = cand[min(c + u, C - 1)];
+                rank += (c + u < C && o > mine) ? 1 : 0;
+            }
         }
         if (lane >= C) rank = lane;  // ranks 0 .. C-1 of the candidates plus the other lanes: a permutation
-        const uint32_t pv = (uint32_t)__builtin_amdgcn_ds_permute(rank * 4, (int)cv);
-        const uint32_t px = (uint32_t)__builtin_amdgcn_ds_permute(rank * 4, (int)cx);
+        const uint32_t pv = (uint32_t)__builtin_amdgcn_ds_permute(rank * 4, (int)(uint32_t)(mine >> 32));
+        const uint32_t px = 0xFFFFFFFFu - (uint32_t)__builtin_amdgcn_ds_permute(rank * 4, (int)(uint32_t)mine);
         top = key_value((uint64_t)__builtin_amdgcn_readfirstlane(pv) << 32);
         if (lane < k) my_v = key_value((uint64_t)pv << 32), my_i = (int)px;
     } else {
