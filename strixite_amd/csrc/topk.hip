@@ -59,7 +59,7 @@ __device__ uint64_t wave_merge_desc(uint64_t a, uint64_t b) {
 // Threshold: the k-th best lane maximum - at least k keys reach it, so every key of the top k does. The keys that
 // reach it (usually ~k: mostly the lane maxima) are compacted through LDS and sorted with one or a few bitonic passes.
 template <int P>
-__device__ uint64_t wave_topk(const uint64_t (&key)[P], int k, uint64_t *scratch, int scratch_cap) {
+__device__ __forceinline__ uint64_t wave_topk_sorted(const uint64_t (&key)[P], int k, uint64_t *scratch, int scratch_cap) {
     const int lane = threadIdx.x & 63;
     uint64_t head = 0;
 #pragma unroll
@@ -100,12 +100,61 @@ __device__ uint64_t wave_topk(const uint64_t (&key)[P], int k, uint64_t *scratch
     return lane < k ? list : 0;
 }
 
+// wave_topk_sorted's result by ranks instead of sorts: the threshold T is the value word of the k-th best lane
+// maximum (a search two bits a step with ballots), so every top-k key has a value word >= T; the keys that reach it
+// (a superset of the top k, ties at T included) go to the wave's LDS row by ballot positions, each takes its rank
+// among them from broadcast reads (keys are unique: ids differ), and the best k land at their ranks. More than 128
+// such keys (heavy ties at T) take the sorting path.
+template <int P>
+__device__ __forceinline__ uint64_t wave_topk(const uint64_t (&key)[P], int k, uint64_t *scratch, int scratch_cap) {
+    const int lane = threadIdx.x & 63;
+    uint64_t head = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) head = umax(head, key[p]);
+    const uint32_t hh = (uint32_t)(head >> 32);
+    uint32_t T = 0u;
+    for (int b = 30; b >= 0; b -= 2) {  // uniform
+        const uint32_t t1 = T | (1u << b), t2 = T | (2u << b), t3 = T | (3u << b);
+        const int c1 = __popcll(__ballot(hh >= t1)), c2 = __popcll(__ballot(hh >= t2)), c3 = __popcll(__ballot(hh >= t3));
+        T = c3 >= k ? t3 : c2 >= k ? t2 : c1 >= k ? t1 : T;
+    }
+    int C = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const bool in = key[p] != 0 && (uint32_t)(key[p] >> 32) >= T;
+        const uint64_t bal = __ballot(in);
+        const int pos = C + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (in && pos < scratch_cap) scratch[pos] = key[p];
+        C += __popcll(bal);
+    }
+    if (C > 128 || C > scratch_cap) return wave_topk_sorted<P>(key, k, scratch, scratch_cap);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const uint64_t a0 = lane < C ? scratch[lane] : 0, a1 = lane + 64 < C ? scratch[lane + 64] : 0;
+    int r0 = 0, r1 = 0;
+    for (int c = 0; c < C; c += 4) {  // uniform
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint64_t o = scratch[min(c + u, C - 1)];
+            const bool valid = c + u < C;
+            r0 += (valid && o > a0) ? 1 : 0;
+            r1 += (valid && o > a1) ? 1 : 0;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // every read above precedes the writes below
+    if (lane < C && r0 < k) scratch[r0] = a0;
+    if (lane + 64 < C && r1 < k) scratch[r1] = a1;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const uint64_t list = lane < min(k, C) ? scratch[lane] : 0;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the row is free for the next use
+    return list;
+}
+
 // ---------------- logits top-k ----------------
 // One level: workgroup g of row r reduces up to kGroup inputs - logits (level 1: ids = positions < n_valid, NaN
 // flagged and left out, masked ids left out) or an earlier level's key lists - to its best k keys. Each wave takes a
 // strided quarter (coalesced loads), finds its best k (wave_topk), and wave 0 merges the four lists.
 constexpr int kTopkThreads = 256;
-constexpr int kPer = 32;                      // inputs a thread holds
+constexpr int kPer = 16;                      // inputs a thread holds
 constexpr int kGroup = kTopkThreads * kPer;   // inputs a workgroup reduces
 constexpr int kScratch = 256;                 // compaction room a wave (keys)
 
@@ -122,20 +171,34 @@ __global__ void __launch_bounds__(kTopkThreads)
     if (t == 0) s_nan = 0;
     uint64_t key[kPer];
     uint32_t my_nan = 0;
+    // every load unconditional (the index clamped into the row) so that all of them go out before the first wait;
+    // a load under a per-lane condition becomes a branch that waits for it
+    if constexpr (kLogits) {
+        float xv[kPer];
+        uint32_t mw[kPer];
 #pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-        const int j = g * kGroup + p * kTopkThreads + t;
-        key[p] = 0;
-        if constexpr (kLogits) {
+        for (int p = 0; p < kPer; ++p) {
+            const int j = min(g * kGroup + p * kTopkThreads + t, n_valid - 1);
+            xv[p] = logits[r * ld + j];
+            if constexpr (kMasked) mw[p] = mask[r * mask_words + (j >> 5)];
+        }
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            const int j = g * kGroup + p * kTopkThreads + t;
+            key[p] = 0;
             if (j < n_valid) {
-                const float x = logits[r * ld + j];
-                const bool allowed = !kMasked || ((mask[r * mask_words + (j >> 5)] >> (j & 31)) & 1u);
+                const float x = xv[p];
+                const bool allowed = !kMasked || ((mw[p] >> (j & 31)) & 1u);
                 if (x != x) my_nan = 1u;  // flagged whether the id is allowed or not
                 else if (allowed) key[p] = cand_key(x, j);
             }
-        } else if (j < n_in) {
-            key[p] = in[r * n_in + j];
         }
+    } else {
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) key[p] = in[r * n_in + min(g * kGroup + p * kTopkThreads + t, n_in - 1)];
+#pragma unroll
+        for (int p = 0; p < kPer; ++p)
+            if (g * kGroup + p * kTopkThreads + t >= n_in) key[p] = 0;
     }
     __syncthreads();
     if (my_nan) atomicOr(&s_nan, 1u);
@@ -157,15 +220,16 @@ __global__ void __launch_bounds__(kTopkThreads)
         else c.id = key_id(best), c.v = logits[r * ld + c.id];
         out_final[r * k + lane] = c;
     }
-    if (lane == 0) {
-        if constexpr (kLogits) {
+    if constexpr (kLogits) {
+        if (lane == 0) {
             nan_level1[r * groups + g] = s_nan;
             if (groups == 1) nan[r] = s_nan;
-        } else if (groups == 1) {
-            uint32_t f = 0;
-            for (int c = 0; c < groups1; ++c) f |= nan_level1[r * groups1 + c];
-            nan[r] = f;
         }
+    } else if (groups == 1) {  // the first level's flags of the row, 64 at a time across the wave
+        bool f = false;
+        for (int c = lane; c < groups1; c += 64) f |= nan_level1[r * groups1 + c] != 0u;
+        const bool any = __ballot(f) != 0;  // the whole wave votes
+        if (lane == 0) nan[r] = any ? 1u : 0u;
     }
 }
 
@@ -231,71 +295,83 @@ __global__ void __launch_bounds__(kPickThreads)
 }
 
 // ---------------- draft acceptance ----------------
-// One lane walks the rows in order, exactly as the engine's loop and the sampler's draw do on the host: the sums are
-// sequential in double, the draw r = u * kept with u the host's generate_canonical<double, 53> for that row.
+// Lane 0 walks the rows in order, exactly as the engine's loop and the sampler's draw do on the host: the sums are
+// sequential in double, the draw r = u * kept with u the host's generate_canonical<double, 53> for that row. The
+// wave loads a row's candidates into LDS and computes their probabilities exp(v_i / T - v_0 / T) a lane each (the
+// same double arithmetic, once each) before lane 0's sequential walk reads them.
 __global__ void __launch_bounds__(64)
     mtp_accept_kernel(const sx_logit_cand *cands, const uint32_t *nan, int kc, const int32_t *drafts, int k,
                       const double *u, double temperature, int top_k, double top_p, int64_t n_valid, int32_t *out) {
-    if (threadIdx.x != 0) return;
+    __shared__ sx_logit_cand cs[64];
+    __shared__ double probs[64];
+    __shared__ int s_go;
+    const int lane = threadIdx.x;
+    const int kk = (int)(top_k < n_valid ? top_k : n_valid);
     int status = 0, j = 0;
     for (;; ++j) {
-        const sx_logit_cand *c = cands + (int64_t)j * kc;
-        int32_t v = -1;
-        bool ok = nan[j] == 0;
-        // serve/sampler.cpp:192-201: real candidates (ids in range) first, then only padding; at least one real.
-        bool padding = false;
-        const int m = kc < 20 ? kc : 20;
-        for (int i = 0; ok && i < m; ++i) {
-            const bool pad = c[i].id == INT32_MAX && c[i].v == -INFINITY;
-            ok = pad || (!padding && c[i].id >= 0 && c[i].id < n_valid);
-            padding |= pad;
-        }
-        ok = ok && c[0].id != INT32_MAX;
-        if (ok && temperature == 0) {
-            v = c[0].id;
-        } else if (ok) {
-            const int kk = (int)(top_k < n_valid ? top_k : n_valid);
-            ok = isfinite(c[0].v);
-            if (ok) {
-                // prob_i recomputed where used (the same double exp each time): no per-lane array in scratch.
-                const double top = (double)c[0].v / temperature;
-                auto prob = [&](int i) { return exp((double)c[i].v / temperature - top); };
-                double sum = 0;
-                for (int i = 0; i < kk; ++i) sum += prob(i);
-                int keep = kk;
-                if (top_p < 1) {
+        if (lane < kc) cs[lane] = cands[(int64_t)j * kc + lane];
+        __syncthreads();
+        if (temperature != 0 && lane < kk && isfinite(cs[0].v))
+            probs[lane] = exp((double)cs[lane].v / temperature - (double)cs[0].v / temperature);
+        __syncthreads();
+        if (lane == 0) {
+            const sx_logit_cand *c = cs;
+            int32_t v = -1;
+            bool ok = nan[j] == 0;
+            // serve/sampler.cpp:192-201: real candidates (ids in range) first, then only padding; at least one real.
+            bool padding = false;
+            const int m = kc < 20 ? kc : 20;
+            for (int i = 0; ok && i < m; ++i) {
+                const bool pad = c[i].id == INT32_MAX && c[i].v == -INFINITY;
+                ok = pad || (!padding && c[i].id >= 0 && c[i].id < n_valid);
+                padding |= pad;
+            }
+            ok = ok && c[0].id != INT32_MAX;
+            if (ok && temperature == 0) {
+                v = c[0].id;
+            } else if (ok) {
+                ok = isfinite(c[0].v);
+                if (ok) {
+                    double sum = 0;
+                    for (int i = 0; i < kk; ++i) sum += probs[i];
+                    int keep = kk;
+                    if (top_p < 1) {
+                        double acc = 0;
+                        for (int i = 0; i < kk; ++i) {
+                            acc += probs[i] / sum;
+                            if (acc >= top_p) {
+                                keep = i + 1;
+                                break;
+                            }
+                        }
+                    }
+                    double kept = 0;
+                    for (int i = 0; i < keep; ++i) kept += probs[i];
+                    const double r = u[j] * kept;
                     double acc = 0;
-                    for (int i = 0; i < kk; ++i) {
-                        acc += prob(i) / sum;
-                        if (acc >= top_p) {
-                            keep = i + 1;
+                    v = c[keep - 1].id;
+                    for (int i = 0; i < keep; ++i) {
+                        acc += probs[i];
+                        if (r < acc) {
+                            v = c[i].id;
                             break;
                         }
                     }
                 }
-                double kept = 0;
-                for (int i = 0; i < keep; ++i) kept += prob(i);
-                const double r = u[j] * kept;
-                double acc = 0;
-                v = c[keep - 1].id;
-                for (int i = 0; i < keep; ++i) {
-                    acc += prob(i);
-                    if (r < acc) {
-                        v = c[i].id;
-                        break;
-                    }
-                }
             }
+            bool go = false;
+            if (!ok) {
+                status = 1 + j;
+            } else {
+                out[2 + j] = v;
+                go = !(j == k || v != drafts[j]);
+            }
+            s_go = go ? 1 : 0;
         }
-        if (!ok) {
-            status = 1 + j;
-            break;
-        }
-        out[2 + j] = v;
-        if (j == k || v != drafts[j]) break;
+        __syncthreads();
+        if (!s_go) break;
     }
-    out[0] = j;
-    out[1] = status;
+    if (lane == 0) out[0] = j, out[1] = status;
 }
 
 }  // namespace
