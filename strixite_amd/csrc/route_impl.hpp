@@ -291,11 +291,21 @@ __device__ void group_in_block(IdAt id_at, int S, int E, int Tmax, int WTmax, in
     for (int b = t; b <= E; b += NT) cnt[b] = 0;
     if (t == 0) *first_bad = INT_MAX;
     __syncthreads();
-    for (int s = t; s < S; s += NT) {
-        const int32_t id = id_at(s);
-        const bool bad = id < 0 || id >= E;
-        atomicAdd(&cnt[bad ? E : id], 1);
-        if (bad) atomicMin(first_bad, s);
+    // ids eight at a time, every load issued before the first use (a load per loop trip would wait each trip)
+    constexpr int kIds = 8;
+    for (int s0 = t; s0 < S; s0 += NT * kIds) {
+        int32_t idv[kIds];
+#pragma unroll
+        for (int u = 0; u < kIds; ++u) idv[u] = id_at(min(s0 + u * NT, S - 1));
+#pragma unroll
+        for (int u = 0; u < kIds; ++u) {
+            const int s = s0 + u * NT;
+            if (s >= S) break;
+            const int32_t id = idv[u];
+            const bool bad = id < 0 || id >= E;
+            atomicAdd(&cnt[bad ? E : id], 1);
+            if (bad) atomicMin(first_bad, s);
+        }
     }
     __syncthreads();
     if (t == 0 && *first_bad != INT_MAX) flag_error(err, (uint32_t)id_at(*first_bad), (uint32_t)*first_bad);
@@ -322,9 +332,17 @@ __device__ void group_in_block(IdAt id_at, int S, int E, int Tmax, int WTmax, in
         offsets[E + 1] = tot[0];
     }
     __syncthreads();
-    for (int s = t; s < S; s += NT) {
-        const int32_t id = id_at(s);
-        slots[atomicAdd(&cursor[(id < 0 || id >= E) ? E : id], 1)] = s;
+    for (int s0 = t; s0 < S; s0 += NT * kIds) {
+        int32_t idv[kIds];
+#pragma unroll
+        for (int u = 0; u < kIds; ++u) idv[u] = id_at(min(s0 + u * NT, S - 1));
+#pragma unroll
+        for (int u = 0; u < kIds; ++u) {
+            const int s = s0 + u * NT;
+            if (s >= S) break;
+            const int32_t id = idv[u];
+            slots[atomicAdd(&cursor[(id < 0 || id >= E) ? E : id], 1)] = s;
+        }
     }
 }
 
