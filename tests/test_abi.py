@@ -65,7 +65,7 @@ def test_route_workspace_layout_contract(L):
 def test_topk_workspace_and_reports(L):
     n = ctypes.c_size_t()
     assert L.sx_logits_topk_workspace_bytes(6, 151936, 40, ctypes.byref(n)) == 0
-    g1 = (151936 + 8191) // 8192
+    g1 = (151936 + 4095) // 4096  # first-level groups of 4096 logits
     assert n.value == 2 * 6 * g1 * 40 * 8 + 6 * g1 * 4
     e = (ctypes.c_uint32 * 3)(1, 700, 5)
     assert L.sx_report_expert_error(e, b"layer 3") == sx.SX_EINVAL
