@@ -37,6 +37,8 @@ def parse():
                          "config-3 gate_up and down kernels alone, and exit")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only config 4's prefill layer (for rocprofv3 runs): one JSON line with its timings")
+    ap.add_argument("--tail-only", action="store_true",
+                    help="only config 5's verify tail (for rocprofv3 runs): one JSON line with its timings")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two --probe counter runs (FETCH_SIZE, WRITE_SIZE) into " + TRAFFIC_JSON)
     return ap.parse_args()
@@ -270,7 +272,6 @@ def extra_configs(out):
 
     from strixite_amd import kernels as kx
     from strixite_amd import synthetic as syn
-    from strixite_amd.verify import VerifyTail
 
     res = {}
     # configs 1 and 2: dense q4 / q8 GEMV, 8 weight replicas rotated (> 256 MB Infinity Cache for config 2)
@@ -287,7 +288,18 @@ def extra_configs(out):
         del reps
     # config 4: the MoE layer at prefill width, M = 2048, Zipf-skewed routing; grouped MFMA experts
     res["cfg4_prefill_layer"] = prefill_layer()
-    # config 5: q8 LM head 151936 x 4096 at M = 6 -> top-40 -> sampled acceptance of 5 drafts
+    res["cfg5_verify_tail"] = verify_tail()
+    out["configs"] = res
+
+
+def verify_tail():
+    """Config 5: q8 LM head 151936 x 4096 at M = 6 -> top-40 -> sampled acceptance of 5 drafts."""
+    import torch
+
+    from strixite_amd import kernels as kx
+    from strixite_amd import synthetic as syn
+    from strixite_amd.verify import VerifyTail
+
     V, d = 151936, 4096
     w = syn.qweight(8, V, d, 64, seed=50)
     h = syn.activations(6, d, seed=51)
@@ -297,10 +309,9 @@ def extra_configs(out):
     ms = time_launches(lambda i: tail.forward(h, drafts, u, 0.7, 40, 0.95), 100)
     ms_head = time_launches(lambda i: kx.linear(h, w, out_act=0, y=tail.logits[:6]), 100)
     nb = w.nbytes() + h.numel() * 2 + 2 * 6 * V * 4
-    res["cfg5_verify_tail"] = {"us": round(ms * 1e3, 3), "lm_head_us": round(ms_head * 1e3, 3),
-                               "lm_head_GBps": round((w.nbytes() + 6 * V * 4) / (ms_head * 1e-3) / 1e9, 1),
-                               "GBps": round(nb / (ms * 1e-3) / 1e9, 1)}
-    out["configs"] = res
+    return {"us": round(ms * 1e3, 3), "lm_head_us": round(ms_head * 1e3, 3),
+            "lm_head_GBps": round((w.nbytes() + 6 * V * 4) / (ms_head * 1e-3) / 1e9, 1),
+            "GBps": round(nb / (ms * 1e-3) / 1e9, 1)}
 
 
 def probe():
@@ -401,6 +412,9 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps({"cfg4_prefill_layer": prefill_layer()}))
+        return
+    if args.tail_only:
+        print(json.dumps({"cfg5_verify_tail": verify_tail()}))
         return
 
     out = {"metric": METRIC, "value": None, "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
