@@ -146,6 +146,16 @@ int sx_logits_topk_workspace_bytes(int64_t rows, int64_t n_valid, int64_t k, siz
 int sx_logits_topk(const float *logits, int64_t rows, int64_t ld, int64_t n_valid, int64_t k, sx_logit_cand *out,
                    uint32_t *nan, void *workspace, size_t workspace_bytes, const uint32_t *mask, int64_t mask_words,
                    sx_stream stream);
+/* sx_logits_topk without a workspace argument and without allocating: the level candidates live in a fixed scratch
+ * array of SX_TOPK_SCRATCH_BYTES the library holds on each device it runs on (until the process ends). No counterpart
+ * in the reference: it is for callers that cannot allocate (HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The same outputs as sx_logits_topk; SX_EINVAL when sx_logits_topk_workspace_bytes for the shape
+ * exceeds the scratch (e.g. 64 rows of 248,320 logits at k = 64 still fit). Calls on one device share the scratch:
+ * two that overlap in time (different streams) race. */
+#define SX_TOPK_SCRATCH_BYTES (4u << 20)
+int sx_logits_topk_noalloc(const float *logits, int64_t rows, int64_t ld, int64_t n_valid, int64_t k,
+                           sx_logit_cand *out, uint32_t *nan, const uint32_t *mask, int64_t mask_words,
+                           sx_stream stream);
 
 /* ---- MTP draft pick, kernels/mtp_pick.hpp:20-33: top-2 + NaN flag + the forward's error words, one 64-byte block.
  * emb_err points at the 8-byte EmbeddingError slot (kernels/embedding.hpp:26-28). ---- */

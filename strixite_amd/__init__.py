@@ -72,6 +72,7 @@ SIGNATURES = {
     "sx_moe_verify_down": [_P, _P, _I64, _I64, _P, _P, _QV, _I64, _P, _INT, _P, _P],
     "sx_logits_topk_workspace_bytes": [_I64, _I64, _I64, _SZP],
     "sx_logits_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_size_t, _P, _I64, _P],
+    "sx_logits_topk_noalloc": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P],
     "sx_mtp_pick": [_P, _I64, _P, _P, _P, _P, _P, _P],
     "sx_mtp_accept": [_P, _P, _I64, _P, _I64, _P, _D, _I64, _D, _I64, _P, _P],
 }

@@ -3,6 +3,8 @@
 #include "common.hpp"
 
 #include <climits>
+#include <mutex>
+#include <vector>
 
 namespace sx {
 namespace {
@@ -375,6 +377,32 @@ __global__ void __launch_bounds__(64)
 }
 
 }  // namespace
+
+// ---------------- fixed scratch of the allocation-free entry point ----------------
+// sx_logits_topk_noalloc keeps its level candidates in this array instead of a caller's workspace: every device the
+// library runs on holds its own copy until the process ends. Its device address comes from hipGetSymbolAddress, once
+// per device with that device current; host code never passes the array's name to a kernel (on the host that name
+// is only a stand-in, not a device address). Nothing in it needs clearing: each level writes every key and flag the
+// next one reads. Calls on one device share it, so two that overlap in time (two streams) race.
+static __device__ __align__(256) uint64_t scratch[SX_TOPK_SCRATCH_BYTES / 8];
+
+int topk_scratch(void **ptr) {
+    static std::mutex mu;
+    static std::vector<void *> per_device;
+    int dev = 0;
+    SX_HIP(hipGetDevice(&dev), "(allocation-free top-k)");
+    std::lock_guard<std::mutex> lock(mu);
+    if ((int)per_device.size() <= dev) per_device.resize(dev + 1, nullptr);
+    if (per_device[dev] == nullptr) {
+        void *p = nullptr;
+        SX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "(device ", dev, ")");
+        per_device[dev] = p;
+    }
+    *ptr = per_device[dev];
+    return SX_OK;
+}
+
+
 }  // namespace sx
 
 using namespace sx;
@@ -435,6 +463,19 @@ int sx_logits_topk(const float *logits, int64_t rows, int64_t ld, int64_t n_vali
         cur = dst, groups = next;
     }
     return SX_OK;
+}
+
+int sx_logits_topk_noalloc(const float *logits, int64_t rows, int64_t ld, int64_t n_valid, int64_t k,
+                           sx_logit_cand *out, uint32_t *nan, const uint32_t *mask, int64_t mask_words,
+                           sx_stream stream) {
+    size_t need = 0;
+    if (int rc = sx_logits_topk_workspace_bytes(rows, n_valid, k, &need)) return rc;
+    SX_CHECK(need <= (size_t)SX_TOPK_SCRATCH_BYTES, "the level candidates of ", rows, " rows of ", n_valid,
+             " logits at k = ", k, " need ", need, " bytes of scratch; the library's fixed scratch holds ",
+             SX_TOPK_SCRATCH_BYTES, " (sx_logits_topk takes a workspace of any size)");
+    void *ws = nullptr;
+    if (int rc = topk_scratch(&ws)) return rc;
+    return sx_logits_topk(logits, rows, ld, n_valid, k, out, nan, ws, need, mask, mask_words, stream);
 }
 
 int sx_mtp_pick(const float *logits, int64_t n, const uint32_t *router_err, const uint32_t *expert_err,

@@ -232,6 +232,17 @@ def logits_topk(logits, n_valid, k=20, mask=None, ws=None, out=None, nan=None, s
     return out[..., 0].view(torch.float32), out[..., 1], nan, out
 
 
+def logits_topk_noalloc(logits, n_valid, k=20, mask=None, out=None, nan=None, stream=None):
+    """logits_topk on the library's fixed scratch (sx_logits_topk_noalloc: no workspace, nothing allocated by the
+    call). Same returns as logits_topk."""
+    rows, ld = logits.shape
+    out = torch.empty((rows, k, 2), dtype=torch.int32, device=logits.device) if out is None else out
+    nan = torch.empty(rows, dtype=torch.int32, device=logits.device) if nan is None else nan
+    mw = 0 if mask is None else mask.shape[1]
+    check(lib().sx_logits_topk_noalloc(_p(logits), rows, ld, n_valid, k, _p(out), _p(nan), _p(mask), mw, _s(stream)))
+    return out[..., 0].view(torch.float32), out[..., 1], nan, out
+
+
 def mtp_pick(logits, router_err, expert_err, attn_err, emb_err, out=None, stream=None):
     out = torch.empty(64, dtype=torch.uint8, device=logits.device) if out is None else out
     check(lib().sx_mtp_pick(_p(logits), logits.numel(), _p(router_err), _p(expert_err), _p(attn_err), _p(emb_err),
