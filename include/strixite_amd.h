@@ -135,6 +135,16 @@ int sx_swiglu(const void *gu, void *h, int64_t rows, int64_t I, int act, sx_stre
 int sx_linear_f32w(const void *x, const float *W, int64_t N, int64_t K, float *y, int64_t M, int act,
                    sx_stream stream);
 
+/* ---- BF16-weight linear, kernels/linear.hpp:14-24 (linear_bf16w) and kernels/linear_wmma.hpp:25-28
+ * (linear_bf16w_wmma): y[M, N] = x[M, K] * W^T, W [N, K] raw BF16 bits row-major, FP32 accumulation, one rounding at
+ * the store; out_act == act, or BF16 x -> F32 y (the router logits of the served model: W [E + 1, d], the shared
+ * expert's gate in the last row, runtime/qwen4exp.cpp:1132-1137). y must not overlap x. _wmma: x rounded to BF16
+ * before the products, K % 64 == 0 and 16-byte aligned x and W (its prefill contract). ---- */
+int sx_linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, int act, int out_act,
+                    sx_stream stream);
+int sx_linear_bf16w_wmma(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, int act,
+                         int out_act, sx_stream stream);
+
 /* ---- logits top-k, kernels/logits_topk.hpp:26-46 ----
  * Per row the best k (value desc, lower id on a tie; -0 ties +0) of ids [0, n_valid); NaN left out and flagged in
  * nan[row]; optional allow mask [rows, mask_words]; padding (-inf, INT32_MAX). k in 1..64 (the reference: 20). */

@@ -149,6 +149,37 @@ void or_linear_f32w(const void *x, const float *W, int64_t N, int64_t K, float *
     });
 }
 
+void or_linear_bf16w(const void *x, const uint16_t *W, int64_t N, int64_t K, void *y, int64_t M, int act,
+                     int out_act, int threads) {
+    std::vector<std::vector<double>> xs;
+    for (int64_t m = 0; m < M; ++m) xs.push_back(widen(x, m * K, K, act));
+    parallel_for(N, threads, [&](int64_t n) {
+        std::vector<float> w((size_t)K);
+        for (int64_t k = 0; k < K; ++k) w[(size_t)k] = bf16f(W[n * K + k]);
+        for (int64_t m = 0; m < M; ++m) store_act(y, m * N + n, (float)dot_d(xs[(size_t)m].data(), w.data(), K), out_act);
+    });
+}
+
+void or_moe_shared_add(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,
+                       uint32_t gate_index, void *x, const float *w_in, int64_t H, int act, uint32_t *err) {
+    for (int64_t m = 0; m < M; ++m) {
+        const float gl = gate_logit[m * gate_ld];
+        const bool ok = std::isfinite(gl);
+        if (!ok) flag(err, (uint32_t)m, gate_index);
+        const float g = ok ? 1.f / (1.f + std::exp(-gl)) : kNaN;
+        for (int64_t n = 0; n < N; ++n) {
+            // y + g * s as one fused multiply-add (the kernel's expression under HIP's default contraction)
+            const float v = as_stored(std::fma(g, load_act(s, m * N + n, act), load_act(y, m * N + n, act)), act);
+            store_act(y, m * N + n, v, act);
+            if (x != nullptr)
+                for (int64_t st = 0; st < H; ++st) {
+                    const int64_t xi = (m * H + st) * N + n;
+                    store_act(x, xi, std::fma(w_in[m * H + st], v, load_act(x, xi, act)), act);
+                }
+        }
+    }
+}
+
 int or_moe_router(const float *logits, int64_t ld, int64_t M, int64_t E, int64_t k, const float *shared,
                   int64_t shared_ld, int32_t shared_id, int32_t *ids, float *coef, uint32_t *err) {
     const int64_t A = k + (shared ? 1 : 0);

@@ -33,6 +33,17 @@ void or_linear_q(int bits, const void *x, const uint8_t *q, const uint16_t *scal
 /* Dense FP32-weight projection (the router logits of the MoE configs): y[M,N] f32 = x[M,K] (act) * W[N,K]^T. */
 void or_linear_f32w(const void *x, const float *W, int64_t N, int64_t K, float *y, int64_t M, int act, int threads);
 
+/* kernels/linear.hpp:14-24 (linear_bf16w; kernels/linear.hip:176-204): y[M,N] = x[M,K] (act) * W^T, W BF16 bits [N, K],
+ * FP32-or-better accumulation (here double), one rounding to out_act (act, or BF16 -> F32). */
+void or_linear_bf16w(const void *x, const uint16_t *W, int64_t N, int64_t K, void *y, int64_t M, int act,
+                     int out_act, int threads);
+
+/* kernels/moe_router.hpp:45-63, moe_router.hip:127-180: y[m,:] = stored(fma(sigmoid(gate_logit[m*gate_ld]), s, y)); a
+ * non-finite gate logit: the row NaN, err {1, m, gate_index} (first wins). x != NULL: then each of the H streams
+ * x[m, st*N + n] = fma(w_in[m*H + st], y_stored, x) rounded once (moe_shared_add_inject). */
+void or_moe_shared_add(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,
+                       uint32_t gate_index, void *x, const float *w_in, int64_t H, int act, uint32_t *err);
+
 /* kernels/moe_router.hpp:11-40: per token the top k of E logits (value desc, index asc), coef = softmax over the k;
  * optional shared slot (sigmoid). Non-finite logit: ids -1, coef NaN, err {1, token, expert}. Returns err[0]. */
 int or_moe_router(const float *logits, int64_t ld, int64_t M, int64_t E, int64_t k, const float *shared,

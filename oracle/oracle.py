@@ -43,6 +43,8 @@ def lib():
         L.or_dequant.argtypes = [_INT, _P, _P, _P, _I64, _I64, _I64, _P]
         L.or_linear_q.argtypes = [_INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _INT, _INT, _INT]
         L.or_linear_f32w.argtypes = [_P, _P, _I64, _I64, _P, _I64, _INT, _INT]
+        L.or_linear_bf16w.argtypes = [_P, _P, _I64, _I64, _P, _I64, _INT, _INT, _INT]
+        L.or_moe_shared_add.argtypes = [_P, _P, _P, _I64, _I64, _I64, ctypes.c_uint32, _P, _P, _I64, _INT, _P]
         L.or_moe_router.argtypes = [_P, _I64, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _P]
         L.or_moe_router.restype = _INT
         for f in (L.or_experts_gather, L.or_experts_gather_swiglu):
@@ -114,6 +116,32 @@ def linear_f32w(x, W, threads=0):
     lib().or_linear_f32w(_ptr(np.ascontiguousarray(x)), _ptr(np.ascontiguousarray(W, np.float32)), N, K, _ptr(y), M,
                          act, threads)
     return y
+
+
+def linear_bf16w(x, W, out_act=None, threads=0):
+    """x [M, K] float32 or BF16 bits, W [N, K] BF16 bits (uint16) -> y [M, N] in out_act (default: x's dtype)."""
+    act = _act_of(x)
+    out_act = act if out_act is None else out_act
+    M, (N, K) = x.shape[0], W.shape
+    y = _new_like(out_act, (M, N))
+    lib().or_linear_bf16w(_ptr(np.ascontiguousarray(x)), _ptr(np.ascontiguousarray(W, np.uint16)), N, K, _ptr(y), M,
+                          act, out_act, threads)
+    return y
+
+
+def moe_shared_add(y, s, gate_logit, gate_ld, gate_index, x=None, w_in=None):
+    """moe_shared_add (x None) or moe_shared_add_inject on host arrays: returns (y', x' or None, err). y, s [M, N] and
+    x [M, H * N] float32 or BF16 bits; gate_logit float32 with row stride gate_ld; w_in float32 [M, H]."""
+    act = _act_of(y)
+    M, N = y.shape
+    y = np.array(y, copy=True)
+    x = None if x is None else np.array(x, copy=True)
+    H = 0 if x is None else x.shape[1] // N
+    err = np.zeros(3, np.uint32)
+    lib().or_moe_shared_add(_ptr(y), _ptr(np.ascontiguousarray(s)), _ptr(np.ascontiguousarray(gate_logit, np.float32)),
+                            gate_ld, M, N, gate_index, _ptr(x),
+                            None if w_in is None else _ptr(np.ascontiguousarray(w_in, np.float32)), H, act, _ptr(err))
+    return y, x, err
 
 
 def moe_router(logits, E, k, shared=None, shared_ld=1, shared_id=0):

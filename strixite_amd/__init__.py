@@ -65,6 +65,8 @@ SIGNATURES = {
     "sx_linear_q4_experts_gather_swiglu_grouped": [_P, _QV, _I64, _P, ctypes.c_size_t, _I64, _I64, _P, _INT, _P],
     "sx_swiglu": [_P, _P, _I64, _I64, _INT, _P],
     "sx_linear_f32w": [_P, _P, _I64, _I64, _P, _I64, _INT, _P],
+    "sx_linear_bf16w": [_P, _P, _P, _I64, _I64, _I64, _INT, _INT, _P],
+    "sx_linear_bf16w_wmma": [_P, _P, _P, _I64, _I64, _I64, _INT, _INT, _P],
     "sx_moe_router_group": [_P, _I64, _I64, _I64, _I64, _INT, _P, _P, _P, _P, ctypes.c_size_t, _P, _P],
     "sx_moe_verify_supported": [_I64, _I64, _I64, _I64, _I64, _QV, _QV, _INT],
     "sx_moe_verify_gate_up": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _INT, _QV, _I64, _P, _P, _P, _P, _INT, _P, _P,

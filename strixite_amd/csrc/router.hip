@@ -154,7 +154,10 @@ __global__ void __launch_bounds__(256) linear_f32w_mfma_kernel(const uint16_t *x
         xb[slot] = *reinterpret_cast<const pw_u32x4 *>(xc + k0);
     };
 #pragma unroll
-    for (int d = 0; d < kPwDepth; ++d) issue(d, d);
+    for (int d = 0; d < kPwDepth; ++d) {
+        issue(d, d);
+        __builtin_amdgcn_sched_barrier(0);  // in slot order, as the loop issues them (exact wait counts at its head)
+    }
     // one K step on ring slot D (a constant: the slots stay in registers)
     auto step = [&](int s0, auto d_tag) __attribute__((always_inline)) {
         constexpr int D = decltype(d_tag)::value, BUF = D & 1;  // kPwDepth is even: the LDS buffer of step s0 + D
@@ -163,6 +166,9 @@ __global__ void __launch_bounds__(256) linear_f32w_mfma_kernel(const uint16_t *x
         *reinterpret_cast<pw_u32x4 *>(&xt[BUF][xs_off]) = xb[D];
         pw_bf16x8 hi, mid, lo;
         split3(wb[D][0], wb[D][1], hi, mid, lo);
+        // a step past the end (the unrolled loop's last round) multiplies zeros: no branch inside the loop, which
+        // would make the wait-count pass wait for every load in flight at the loop head
+        if (s0 + D >= nk) hi = pw_bf16x8{}, mid = pw_bf16x8{}, lo = pw_bf16x8{};
         __builtin_amdgcn_sched_barrier(0);  // the reload stays after the last use of the slot
         issue(s0 + D + kPwDepth, D);
         // the tile of this step is complete; the other buffer's reads (the step before) are done. LDS-only fences:
@@ -170,14 +176,12 @@ __global__ void __launch_bounds__(256) linear_f32w_mfma_kernel(const uint16_t *x
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        if (s0 + D < nk) {  // uniform
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const pw_bf16x8 A = *reinterpret_cast<const pw_bf16x8 *>(&xt[BUF][(tt * 16 + n16) * kPwLd + g * 8]);
-                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, lo, acc[tt], 0, 0, 0);
-                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, mid, acc[tt], 0, 0, 0);
-                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, hi, acc[tt], 0, 0, 0);
-            }
+        for (int tt = 0; tt < 4; ++tt) {
+            const pw_bf16x8 A = *reinterpret_cast<const pw_bf16x8 *>(&xt[BUF][(tt * 16 + n16) * kPwLd + g * 8]);
+            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, lo, acc[tt], 0, 0, 0);
+            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, mid, acc[tt], 0, 0, 0);
+            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, hi, acc[tt], 0, 0, 0);
         }
     };
     static_assert(kPwDepth == 4, "the K loop below is unrolled by four");
@@ -187,6 +191,7 @@ __global__ void __launch_bounds__(256) linear_f32w_mfma_kernel(const uint16_t *x
         step(s0, std::integral_constant<int, 2>{});
         step(s0, std::integral_constant<int, 3>{});
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the wave exits
     if (row >= N) return;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)

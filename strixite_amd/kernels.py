@@ -213,6 +213,32 @@ def linear_f32w(x, W, y=None, stream=None):
     return y
 
 
+def linear_bf16w(x, W, out_act=None, y=None, wmma=False, stream=None):
+    """y[M, N] = x[M, K] * W^T with W BF16 [N, K] (linear_bf16w; wmma: linear_bf16w_wmma, x rounded to BF16)."""
+    act = act_of(x)
+    out_act = act if out_act is None else out_act
+    M, K = x.shape
+    N = W.shape[0]
+    y = torch.empty((M, N), dtype=dtype_of(out_act), device=x.device) if y is None else y
+    f = lib().sx_linear_bf16w_wmma if wmma else lib().sx_linear_bf16w
+    check(f(_p(x), _p(W), _p(y), M, N, K, act, out_act, _s(stream)))
+    return y
+
+
+def moe_shared_add(y, s, gate_logit, gate_index, err, x=None, w_in=None, stream=None):
+    """moe_shared_add (x None) or moe_shared_add_inject, in place on y (and x [M, H * N]). gate_logit: FP32 column
+    view (row stride = its stride(0))."""
+    M, N = y.shape
+    gl = gate_logit.stride(0)
+    if x is None:
+        check(lib().sx_moe_shared_add(_p(y), _p(s), _p(gate_logit), gl, M, N, gate_index, act_of(y), _p(err),
+                                      _s(stream)))
+    else:
+        check(lib().sx_moe_shared_add_inject(_p(y), _p(s), _p(gate_logit), gl, M, N, gate_index, _p(x), _p(w_in),
+                                             x.shape[1] // N, act_of(y), _p(err), _s(stream)))
+    return y
+
+
 def topk_workspace_bytes(rows, n_valid, k):
     n = ctypes.c_size_t()
     check(lib().sx_logits_topk_workspace_bytes(rows, n_valid, k, ctypes.byref(n)))

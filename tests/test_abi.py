@@ -29,6 +29,24 @@ def test_header_and_python_signatures_agree():
     assert declared() == set(sx.SIGNATURES), declared() ^ set(sx.SIGNATURES)
 
 
+def declared_arity():
+    """name -> number of parameters, parsed from the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:int|const char \*)\s*(sx_\w+)\s*\(([^;]*?)\)\s*;", text, re.M | re.S):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_python_argtypes_match_header_arity():
+    """Each ctypes signature has as many arguments as the C prototype (a dropped pointer would shift the rest)."""
+    ar = declared_arity()
+    assert set(ar) == declared()
+    for name, n in ar.items():
+        assert len(sx.SIGNATURES[name]) == n, f"{name}: {len(sx.SIGNATURES[name])} argtypes, header has {n}"
+
+
 def test_every_declared_symbol_is_exported(L):
     for name in declared():
         assert hasattr(L, name), name

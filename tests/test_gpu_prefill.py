@@ -1,0 +1,111 @@
+"""BASELINE config 4 at full size on cuda:0 through the C ABI: the MoE layer at prefill width (M = 2048 tokens,
+d = 4096, E = 512, top-10, I = 1024, q4 G = 128, routing skewed by a seeded Zipf(1.1) bias), and the dense linears at
+prefill width (the route the reference's linear_q4_wmma / linear_q8_wmma callers take, kernels/linear_wmma.hpp:22-25).
+
+The oracle recomputes the router logits in full, the routing bit-exact on the GPU's logits, the grouping invariants
+on all 20,480 slots, and h and y for a seeded sample of tokens (every expert those tokens touch)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import util
+
+pytestmark = pytest.mark.gpu
+
+
+def kx():
+    from strixite_amd import kernels
+    return kernels
+
+
+def sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def test_config4_prefill_layer_full_size():
+    import torch
+    from strixite_amd import synthetic as syn
+    E, d, I, k, M = 512, 4096, 1024, 10, 2048
+    print("config 4: building inputs", flush=True)
+    Wr = syn.router_weight(E, d, seed=61)
+    gu = syn.qweight(4, E * 2 * I, d, 128, seed=62)
+    dn = syn.qweight(4, E * d, I, 128, seed=63)
+    bias = syn.zipf_router_bias(E, seed=64)
+    x = syn.activations(M, d, seed=65)
+
+    print("config 4: router projection + Zipf bias + routing + grouping", flush=True)
+    logits = kx().linear_f32w(x, Wr)
+    raw = logits.clone()
+    logits.add_(bias)
+    ids, coef, rerr = kx().moe_router(logits, E, k)
+    ws, eerr = kx().group_routes(ids, E)
+    print("config 4: grouped gate_up + SwiGLU, grouped down + combine", flush=True)
+    h = kx().gather_grouped(x, gu, E, ws, M, k, swiglu=True)
+    y = kx().combine_grouped(h, dn, E, ids, coef, ws)
+    sync()
+
+    xh = util.host_bits(x)
+    util.assert_close(raw.cpu().numpy(), orc.linear_f32w(xh, Wr.cpu().numpy()), tol=1e-5, what="router logits")
+    L = logits.cpu().numpy()
+    ref_ids, ref_coef, _ = orc.moe_router(L, E, k)
+    g_ids = ids.cpu().numpy()
+    assert np.array_equal(g_ids, ref_ids), "expert ids differ from the oracle on the same logits"
+    util.assert_close(coef.cpu().numpy(), ref_coef, tol=1e-6, what="coef")
+    assert rerr.cpu().numpy()[0] == 0 and eerr.cpu().numpy()[0] == 0
+
+    # grouping: the workspace layout of kernels/moe_grouped.hip:63-81 on 20,480 slots
+    S = M * k
+    w = ws.cpu().numpy()
+    Tmax, WTmax = S // 16 + E + 2, S // 64 + E + 2
+    off = w[4:4 + E + 2]
+    slots = w[4 + E + 2:4 + E + 2 + S]
+    counts = np.bincount(g_ids.ravel(), minlength=E + 1)
+    assert list(w[1:3]) == [S, E]
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(counts)]))
+    assert np.array_equal(np.sort(slots), np.arange(S))
+    for b in range(E):
+        assert np.all(g_ids.ravel()[slots[off[b]:off[b + 1]]] == b)
+    t = 4 + E + 2 + S
+    for R, n, tb, ts in ((16, w[0], w[t:t + Tmax], w[t + Tmax:t + 2 * Tmax]),
+                         (64, w[3], w[t + 2 * Tmax:t + 2 * Tmax + WTmax], w[t + 2 * Tmax + WTmax:t + 2 * Tmax + 2 * WTmax])):
+        assert n == sum((c + R - 1) // R for c in counts)
+        for b in np.flatnonzero(counts):
+            assert list(ts[:n][tb[:n] == b]) == list(range(off[b], off[b + 1], R))
+    print(f"config 4: {int((counts[:E] > 0).sum())} experts used, buckets 0..{int(counts[:E].max())} slots, "
+          f"{int((counts[:E] > 64).sum())} over one 64-slot tile", flush=True)
+    assert counts[:E].max() > 128  # Zipf: a hot head of experts over two wide tiles
+
+    # h and y for a seeded sample of tokens, against the oracle on the touched experts' rows
+    toks = np.sort(np.random.default_rng(66).choice(M, 32, replace=False))
+    sub = g_ids[toks]
+    touched = np.unique(sub)
+    U = len(touched)
+    rid = np.searchsorted(touched, sub).astype(np.int32)
+    print(f"config 4: checking h and y of {len(toks)} tokens over {U} experts", flush=True)
+    cat = lambda wt, rows: [np.concatenate(p) for p in zip(*[syn.host_rows(wt, e * rows, (e + 1) * rows) for e in touched])]
+    hgu = orc.QWeight(4, *cat(gu, 2 * I), U * 2 * I, d, 128)
+    ref_h, _ = orc.experts_gather(xh[toks], hgu, U, rid, swiglu=True)
+    gh = util.host_bits(h)[toks]
+    util.assert_close(gh, ref_h, roundings=4, what="config 4 h (sampled tokens)")
+    del hgu
+    hdn = orc.QWeight(4, *cat(dn, d), U * d, I, 128)
+    ref_y, _ = orc.experts_combine(gh, hdn, U, rid, coef.cpu().numpy()[toks])
+    util.assert_close(util.host_bits(y)[toks], ref_y, what="config 4 y (sampled tokens)")
+
+
+@pytest.mark.parametrize("bits,G,act,out_act", [(4, 128, orc.BF16, orc.BF16), (8, 64, orc.BF16, orc.F32),
+                                               (4, 128, orc.F32, orc.F32)])
+def test_dense_linear_prefill_width(bits, G, act, out_act):
+    """linear_q4 / linear_q8 at M = 2048 (the prefill-width route *_wmma callers take) against the oracle."""
+    M, N, K = 2048, 384, 4096
+    rng = np.random.default_rng(bits * 10 + act)
+    w = util.rand_qweight(rng, bits, N, K, G)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x = x if act == orc.F32 else util.f32_to_bf16(x)
+    print(f"dense prefill q{bits} G{G} act={act} out={out_act}", flush=True)
+    xd = util.f32_dev(x) if act == orc.F32 else util.bf16_dev(x)
+    y = kx().linear(xd, kx().QWeight.upload(w), out_act=out_act)
+    sync()
+    ref = orc.linear_q(x, w, out_act=out_act)
+    util.assert_close(util.host_bits(y), ref, what=f"dense q{bits} M={M}")

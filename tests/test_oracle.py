@@ -97,6 +97,75 @@ def test_linear_f32w_basis_vectors_and_brute_force():
                                atol=1e-7)
 
 
+def test_linear_bf16w_basis_vectors_and_brute_force():
+    """The BF16-weight projection (linear_bf16w): x = e_k returns column k of W exactly (in F32 and, rounded once, in
+    BF16), and random x agrees with a float64 product of the widened weights; a transposed W or a byte-swapped BF16
+    decode fails both."""
+    rng = np.random.default_rng(19)
+    W = util.f32_to_bf16((rng.standard_normal((24, 96)) * 0.02).astype(np.float32))
+    Wf = util.bf16_to_f32(W)
+    for k in (0, 7, 95):
+        x = np.zeros((1, 96), np.float32)
+        x[0, k] = 1.0
+        assert np.array_equal(orc.linear_bf16w(x, W)[0], Wf[:, k])
+        assert np.array_equal(orc.linear_bf16w(util.f32_to_bf16(x), W)[0], W[:, k])           # BF16 out: same bits
+        assert np.array_equal(orc.linear_bf16w(util.f32_to_bf16(x), W, out_act=orc.F32)[0], Wf[:, k])
+    x = rng.standard_normal((5, 96)).astype(np.float32)
+    np.testing.assert_allclose(orc.linear_bf16w(x, W), x.astype(np.float64) @ Wf.astype(np.float64).T, rtol=1e-6,
+                               atol=1e-7)
+
+
+def test_shared_add_closed_forms():
+    """moe_shared_add: gate logit 0 gives sigmoid 1/2 exactly, so y + s/2 is exact for representable halves; a large
+    negative gate leaves y unchanged; a non-finite gate makes the row NaN and names (token, gate_index) - the first
+    such token only; the inject form adds w_in[s] * y_stored to each of the H = 4 streams (checked in float64)."""
+    M, N = 4, 32
+    y = np.arange(M * N, dtype=np.float32).reshape(M, N) / 8
+    s = np.full((M, N), 2.0, np.float32)
+    gl = np.array([0.0, -200.0, np.inf, np.nan], np.float32)
+    y2, _, err = orc.moe_shared_add(y, s, gl, 1, 512)
+    assert np.array_equal(y2[0], y[0] + 1.0)
+    assert np.array_equal(y2[1], y[1])
+    assert np.isnan(y2[2]).all() and np.isnan(y2[3]).all()
+    assert list(err) == [1, 2, 512]
+    # BF16, strided gate column, inject into 4 streams
+    rng = np.random.default_rng(20)
+    yb = util.f32_to_bf16(rng.standard_normal((M, N)).astype(np.float32))
+    sb = util.f32_to_bf16(rng.standard_normal((M, N)).astype(np.float32))
+    G = rng.standard_normal((M, 3)).astype(np.float32)  # the gate logit in column 2 of rows of 3
+    xb = util.f32_to_bf16(rng.standard_normal((M, 4 * N)).astype(np.float32))
+    w_in = rng.standard_normal((M, 4)).astype(np.float32)
+    y3, x3, err = orc.moe_shared_add(yb, sb, G.ravel()[2:], 3, 7, x=xb, w_in=w_in)
+    assert list(err) == [0, 0, 0]
+    g = 1 / (1 + np.exp(-G[:, 2].astype(np.float64)))
+    want_y = util.bf16_to_f32(yb) + g[:, None] * util.bf16_to_f32(sb)
+    got_y = util.bf16_to_f32(y3).astype(np.float64)
+    assert np.all(np.abs(got_y - want_y) <= 2.0 ** -8 * np.abs(want_y) + 1e-30)
+    want_x = util.bf16_to_f32(xb).reshape(M, 4, N) + w_in[:, :, None] * got_y[:, None, :]
+    got_x = util.bf16_to_f32(x3).reshape(M, 4, N)
+    assert np.all(np.abs(got_x - want_x) <= 2.0 ** -8 * np.abs(want_x) + 1e-30)
+
+
+def test_assert_close_catches_a_one_percent_bias():
+    """The GPU tests' tolerance check: unbiased one-ulp rounding differences pass; a 1 % error in every element fails
+    it although each element alone stays inside the per-element BF16 bound; a few elements off by several ulps pass
+    only while they stay under 0.1 %."""
+    rng = np.random.default_rng(21)
+    ref = rng.standard_normal(20000).astype(np.float32)
+    ref_b = util.f32_to_bf16(ref)
+    flip = rng.random(ref.size) < 0.3
+    near = util.f32_to_bf16(util.bf16_to_f32(ref_b) * np.where(flip, 1 + 2.0 ** -9, 1.0).astype(np.float32))
+    util.assert_close(near, ref_b, roundings=4)
+    biased = util.f32_to_bf16(ref * 1.01)
+    with pytest.raises(AssertionError):
+        util.assert_close(biased, ref_b, roundings=4)
+    off = util.bf16_to_f32(ref_b).copy()
+    idx = rng.choice(ref.size, 30, replace=False)
+    off[idx] *= 1.02
+    with pytest.raises(AssertionError, match="differ by more than one"):
+        util.assert_close(util.f32_to_bf16(off), ref_b, roundings=4)
+
+
 def test_swiglu_limits_and_bf16_rounding_points():
     """silu(v) = v / (1 + e^-v): 0 at 0, v for large v, -0 side for very negative v, silu(1) = 1/(1 + 1/e); a swapped
     gate / up or a missing sigmoid fails. BF16 rounds twice: bf16(bf16(silu(g)) * u) (kernels/swiglu.hip:31-36)."""

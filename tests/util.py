@@ -68,11 +68,24 @@ def as_f32(a):
     return bf16_to_f32(a) if a.dtype == np.uint16 else np.asarray(a, np.float32)
 
 
-def assert_close(got, ref, tol=1e-3, what="", roundings=1):
-    """The north star's bar: max |got - ref| <= tol * max |ref| (FP32 outputs). BF16 outputs (uint16 bits) may also
-    differ by the roundings to BF16 along the way: + roundings * 2^-8 |ref| per element (1: the store; SwiGLU of
-    stored gate and up: gate, up, silu and the product, 4). A BF16 reference was rounded once more on its own side:
-    two FP32 values a hair apart can round to neighbouring BF16 values, up to 2 x 2^-8 |ref| apart."""
+def bf16_ulp(r):
+    """One BF16 unit in the last place at |r| (8 significant bits): 2^(floor(log2 |r|) - 7); zero maps to the smallest
+    normal's ulp."""
+    a = np.maximum(np.abs(np.asarray(r, np.float64)), 2.0 ** -126)
+    return np.exp2(np.floor(np.log2(a)) - 7)
+
+
+def assert_close(got, ref, tol=1e-3, what="", roundings=1, max_off_frac=1e-3, max_bias=1e-4):
+    """The north star's bar, plus two checks that catch a systematic error the per-element bound would let through.
+
+    1. Per element: max |got - ref| <= tol * max |ref| (FP32 outputs). BF16 outputs (uint16 bits) may also differ by the
+       roundings to BF16 along the way: + roundings * 2^-8 |ref| per element (1: the store; SwiGLU of stored gate and
+       up: gate, up, silu and the product, 4). A BF16 reference was rounded once more on its own side: two FP32 values
+       a hair apart can round to neighbouring BF16 values, up to 2 x 2^-8 |ref| apart.
+    2. At most max_off_frac of the elements (at least one) differ by more than one BF16 ulp of the reference plus
+       tol / 10 of max |ref| (a value that differs only by summation order is off by far less).
+    3. The mean signed error over all elements is below max_bias * max |ref|, widened for small arrays by three
+       standard errors of unbiased BF16 rounding (2^-8 mean |ref| / sqrt(n)): a bias of 1 % in every element fails."""
     g = as_f32(got).astype(np.float64)
     r = as_f32(ref).astype(np.float64)
     assert g.shape == r.shape, (g.shape, r.shape)
@@ -89,6 +102,14 @@ def assert_close(got, ref, tol=1e-3, what="", roundings=1):
         bound = tol * scale + roundings * 2.0 ** -8 * np.abs(r[ok])
     else:
         bound = tol * scale
-    err = np.abs(g[ok] - r[ok])
+    diff = g[ok] - r[ok]
+    err = np.abs(diff)
     worst = float(np.max(err / scale))
     assert np.all(err <= bound), f"{what}: max-abs-normalised error {worst:.3g} over tolerance {tol}"
+    off = int(np.count_nonzero(err > bf16_ulp(r[ok]) + 0.1 * tol * scale))
+    allowed = max(1, int(max_off_frac * err.size))
+    assert off <= allowed, (f"{what}: {off} of {err.size} elements ({off / err.size:.2%}) differ by more than one "
+                            f"BF16 ulp; at most {allowed} allowed")
+    bias = float(np.mean(diff)) / scale
+    limit = max_bias + 3 * 2.0 ** -8 * float(np.mean(np.abs(r[ok]))) / scale / np.sqrt(err.size)
+    assert abs(bias) <= limit, f"{what}: mean signed error {bias:.3g} of max |ref| (limit {limit:.3g})"
