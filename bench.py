@@ -1,13 +1,14 @@
 """Benchmark of strixite's MTP verify path on one MI355X (BASELINE.json's metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extra]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 
 A step is one MoE FFN verify sublayer: M = 6 tokens, hidden 4096, 512 experts, top-10 routing
 from FP32 router logits, SwiGLU experts (gate_up [1024 x 2 x 4096], down [4096 x 1024]) in q4 G = 128. Each step takes
 the next of 16 distinct token batches (different routing each, so the 3.4 GB of experts are not served from the
 256 MB Infinity Cache), with every input resident in HBM before the timed region. One JSON line goes to stdout:
 value = microseconds per layer; roofline = the grouped gate_up + SwiGLU kernel (the dominant one) timed with HIP events
-on its stream; cpu_baseline = the CPU oracle's same layer on this host's cores. --extra adds configs 1, 2 and 5.
+on its stream over a fixed window; cpu_baseline = the CPU oracle's same layer on this host's cores. The line also
+carries config 4's prefill tok/s and MFMA fraction and configs 1, 2 and 5 (skip them with --no-extra).
 """
 import argparse
 import json
@@ -30,7 +31,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
-    ap.add_argument("--extra", action="store_true", help="also time configs 1, 2 and 5")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 1, 2, 4 (prefill tok/s) and 5")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--probe", action="store_true",
                     help="for rocprofv3 --pmc: a plain copy kernel of known size (the counters' calibration), then the "
@@ -49,19 +50,39 @@ def events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_launches(fn, n, warm=5):
-    """Average milliseconds of fn() over n back-to-back launches on torch's current stream (HIP events)."""
+def time_window(fn, min_launches=400, min_ms=25.0, warm_ms=25.0, windows=5):
+    """Milliseconds a launch of fn(i), independent of --steps: launches run for warm_ms (and at least 100) to settle
+    the clocks, then `windows` timed windows of at least min_launches launches and min_ms each (HIP events on torch's
+    current stream, the stream the kernels run on); the median window's average."""
+    import time as _t
+
     import torch
-    for i in range(warm):
+    i = 0
+    t0 = _t.perf_counter()
+    while i < 100 or (_t.perf_counter() - t0) * 1e3 < warm_ms:
         fn(i)
+        i += 1
+        if i % 50 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
-    a, b = events()
-    a.record()
-    for i in range(n):
-        fn(i)
-    b.record()
-    b.synchronize()
-    return a.elapsed_time(b) / n
+    per = []
+    for _ in range(windows):
+        n = min_launches
+        while True:
+            a, b = events()
+            a.record()
+            for _j in range(n):
+                fn(i)
+                i += 1
+            b.record()
+            b.synchronize()
+            ms = a.elapsed_time(b)
+            if ms >= min_ms:
+                break
+            n *= 2
+        per.append(ms / n)
+    per.sort()
+    return per[len(per) // 2]
 
 
 def gate_up_bytes(U, per_expert, M, d, E, k, I):
@@ -104,7 +125,16 @@ def moe_layer_bench(args, out):
         bytes_layer.append(U * per_expert + Wr.numel() * 4 + 2 * M * d * 2)
     torch.cuda.synchronize()
 
-    # the timed steps: whole layers, rotating the batches
+    # the timed steps: whole layers, rotating the batches. Before the W warm-up steps the layer runs for ~30 ms
+    # (untimed) so that the clocks have left their idle state whatever W is.
+    t_settle = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t_settle < 0.03 or i < 64:
+        layer.forward(xs[i % R])
+        i += 1
+        if i % 64 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
     for i in range(args.warmup):
         layer.forward(xs[i % R])
     torch.cuda.synchronize()
@@ -137,9 +167,8 @@ def moe_layer_bench(args, out):
         kx.verify_gate_up(xs[i % R], routes[i % R][3], gu, E, k, ids=ids_b, coef=coef_b, h=h, router_err=rerr,
                           expert_err=eerr, h_sums=h_sums)
 
-    n = max(args.steps, 64)
-    ms = time_launches(gate_up, n)
-    gu_bytes = sum(gate_up_bytes(Us[i % R], gu_per_expert, M, d, E, k, I) for i in range(n)) / n
+    ms = time_window(gate_up)
+    gu_bytes = sum(gate_up_bytes(Us[r], gu_per_expert, M, d, E, k, I) for r in range(R)) / R
     achieved = gu_bytes / (ms * 1e-3) / 1e9
     traffic = None
     tj = os.path.join(ROOT, TRAFFIC_JSON)
@@ -159,15 +188,27 @@ def moe_layer_bench(args, out):
     def down(i):
         kx.verify_down(hh[i % R], dn, routes[i % R][0], routes[i % R][1], E, y=yb, expert_err=eerr, h_sums=hs[i % R])
 
-    ms_dn = time_launches(down, n)
-    dn_bytes = sum(down_bytes(Us[i % R], dn.nbytes() // E, M, d, k, I) for i in range(n)) / n
+    ms_dn = time_window(down)
+    dn_bytes = sum(down_bytes(Us[r], dn.nbytes() // E, M, d, k, I) for r in range(R)) / R
     out["down_combine"] = {"avg_us": round(ms_dn * 1e3, 3), "GBps": round(dn_bytes / (ms_dn * 1e-3) / 1e9, 1)}
     return layer, xs, routes
 
 
-def cpu_baseline(layer, xs, budget_s):
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(layer, xs, budget_s, gpu_logits):
     """The CPU oracle's same layer (router projection, top-k, SwiGLU experts, combine; FP64 accumulation) on this
-    host's cores, over as many of the token batches as fit the time budget."""
+    host's cores, over as many of the token batches as fit the time budget, then one batch on a single thread. Also
+    counts the tokens whose top-k set differs when routing uses the CPU's own logits instead of the GPU's (near-ties
+    of the FP32 projection), over every batch."""
     import numpy as np
     import torch
 
@@ -176,36 +217,52 @@ def cpu_baseline(layer, xs, budget_s):
 
     E, k, d, I = layer.E, layer.k, layer.d, layer.I
     Wr = layer.Wr.cpu().numpy()
-    threads = min(os.cpu_count() or 1, 16)  # the GPU box's CPU share
-    done, t_total = 0, 0.0
+    nproc = os.cpu_count() or 1
+    threads = min(nproc, 16)  # the GPU box's CPU share for one GPU, whatever nproc reports
     cache = {}
+    prepared = []
+    flips = 0
     for r, x in enumerate(xs):
         xh = x.view(torch.int16).cpu().numpy().view(np.uint16)
-        # weights the batch touches, copied to the host before the clock starts (they are resident in RAM on a host)
         logits = orc.linear_f32w(xh, Wr)
         ids, coef, _ = orc.moe_router(logits, E, k)
+        g_ids, _, _ = orc.moe_router(gpu_logits[r], E, k)
+        flips += int((np.sort(ids, 1) != np.sort(g_ids, 1)).any(1).sum())
+        prepared.append((xh, ids))
+
+    def run(r, nthreads):
+        xh, ids = prepared[r]
+        # the experts the batch touches, copied to the host before the clock starts (resident in RAM on a host)
         touched = [int(e) for e in np.unique(ids)]
         for e in touched:
             if e not in cache:
-                cache[e] = (syn.host_rows(layer.gate_up, e * 2 * I, (e + 1) * 2 * I), syn.host_rows(layer.down, e * d, (e + 1) * d))
+                cache[e] = (syn.host_rows(layer.gate_up, e * 2 * I, (e + 1) * 2 * I),
+                            syn.host_rows(layer.down, e * d, (e + 1) * d))
         remap = {e: i for i, e in enumerate(touched)}
         U = len(touched)
         cat = lambda j, z: np.concatenate([cache[e][j][z] for e in touched])
         hgu = orc.QWeight(4, cat(0, 0), cat(0, 1), cat(0, 2), U * 2 * I, d, 128)
         hdn = orc.QWeight(4, cat(1, 0), cat(1, 1), cat(1, 2), U * d, I, 128)
         t0 = time.perf_counter()
-        logits = orc.linear_f32w(xh, Wr, threads=threads)
-        ids, coef, _ = orc.moe_router(logits, E, k)
-        rid = np.vectorize(remap.get)(ids).astype(np.int32)
-        h, _ = orc.experts_gather(xh, hgu, U, rid, swiglu=True, threads=threads)
-        orc.experts_combine(h, hdn, U, rid, coef, threads=threads)
-        t_total += time.perf_counter() - t0
-        done += 1
-        if t_total >= budget_s:
+        logits = orc.linear_f32w(xh, Wr, threads=nthreads)
+        ids2, coef, _ = orc.moe_router(logits, E, k)
+        rid = np.vectorize(remap.get)(ids2).astype(np.int32)
+        h, _ = orc.experts_gather(xh, hgu, U, rid, swiglu=True, threads=nthreads)
+        orc.experts_combine(h, hdn, U, rid, coef, threads=nthreads)
+        return time.perf_counter() - t0
+
+    times = []
+    for r in range(len(xs)):
+        times.append(run(r, threads))
+        if sum(times) >= budget_s:
             break
-    return {"value": round(t_total / done * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"{done} of the {len(xs)} token batches (M = 6 each) through the CPU oracle's layer, "
-                      f"FP64 accumulation, {threads} threads"}
+    t1 = run(0, 1)
+    med = sorted(times)[len(times) // 2]
+    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "single_thread_us": round(t1 * 1e6, 1), "nproc": nproc, "cpu_model": cpu_model(),
+            "sample": f"{len(times)} of the {len(xs)} token batches (M = 6 each) through the CPU oracle's layer "
+                      f"(median), FP64 accumulation, {threads} threads; single_thread_us: batch 0 on one thread",
+            "routing_flips_cpu_vs_gpu_logits": {"tokens": flips, "of": len(xs) * xs[0].shape[0]}}
 
 
 def prefill_layer(steps=20):
@@ -251,7 +308,7 @@ def prefill_layer(steps=20):
             ev[3].record()
             stamps[i] = ev
 
-    ms = time_launches(layer, steps, warm=3)
+    ms = time_window(layer, min_launches=steps, min_ms=30.0, windows=3)
     layer(0, mark=True)
     torch.cuda.synchronize()
     ev = stamps[0]
@@ -281,7 +338,7 @@ def extra_configs(out):
         reps = [syn.qweight(bits, N, K, G, seed=30 + i) for i in range(8 if N > 4096 else 32)]
         x = syn.activations(M, K, seed=40, dtype=act)
         y = torch.empty((M, N), dtype=torch.float32, device="cuda")
-        ms = time_launches(lambda i: kx.linear(x, reps[i % len(reps)], out_act=0, y=y), 400)
+        ms = time_window(lambda i: kx.linear(x, reps[i % len(reps)], out_act=0, y=y))
         nbytes = reps[0].nbytes() + x.numel() * x.element_size() + y.numel() * 4
         res[name] = {"us": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                      "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -306,8 +363,8 @@ def verify_tail():
     tail = VerifyTail(w, V, 40, 6)
     drafts = torch.randint(0, V, (5,), dtype=torch.int32, device="cuda")
     u = torch.rand(6, dtype=torch.float64, device="cuda")
-    ms = time_launches(lambda i: tail.forward(h, drafts, u, 0.7, 40, 0.95), 100)
-    ms_head = time_launches(lambda i: kx.linear(h, w, out_act=0, y=tail.logits[:6]), 100)
+    ms = time_window(lambda i: tail.forward(h, drafts, u, 0.7, 40, 0.95), min_launches=100, windows=3)
+    ms_head = time_window(lambda i: kx.linear(h, w, out_act=0, y=tail.logits[:6]), min_launches=100, windows=3)
     nb = w.nbytes() + h.numel() * 2 + 2 * 6 * V * 4
     return {"us": round(ms * 1e3, 3), "lm_head_us": round(ms_head * 1e3, 3),
             "lm_head_GBps": round((w.nbytes() + 6 * V * 4) / (ms_head * 1e-3) / 1e9, 1),
@@ -426,11 +483,14 @@ def main():
     layer, xs, routes = moe_layer_bench(args, out)
     print(f"moe layer: {out['value']} us/layer, {out['layer_GBps']} GB/s; gate_up kernel "
           f"{out['roofline']['achieved']} GB/s", file=sys.stderr, flush=True)
-    if args.extra:
+    if not args.no_extra:
         extra_configs(out)
+        pf = out["configs"]["cfg4_prefill_layer"]
+        out["prefill_tok_per_s"] = pf["prefill_tok_per_s"]
+        out["prefill_mfma_frac"] = pf["mfma_frac"]
         print(f"configs: {json.dumps(out['configs'])}", file=sys.stderr, flush=True)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(layer, xs, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(layer, xs, args.cpu_seconds, [r[3].cpu().numpy() for r in routes])
     print(json.dumps(out), flush=True)
 
 
