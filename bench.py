@@ -191,6 +191,20 @@ def moe_layer_bench(args, out):
     ms_dn = time_window(down)
     dn_bytes = sum(down_bytes(Us[r], dn.nbytes() // E, M, d, k, I) for r in range(R)) / R
     out["down_combine"] = {"avg_us": round(ms_dn * 1e3, 3), "GBps": round(dn_bytes / (ms_dn * 1e-3) / 1e9, 1)}
+
+    # the same layer as one launch (sx_moe_verify_layer: projection, routing, gate_up and down as phases of one
+    # kernel), over the same rotating batches
+    sy = kx.verify_layer_sync()
+    lg = torch.empty((M, E), dtype=torch.float32, device="cuda")
+    yl = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
+
+    def one_launch(i):
+        kx.verify_layer(xs[i % R], Wr, gu, dn, E, k, sy, logits=lg, ids=ids_b, coef=coef_b, h=h, h_sums=h_sums, y=yl,
+                        router_err=rerr, expert_err=eerr)
+
+    ms_one = time_window(one_launch)
+    out["one_launch_layer"] = {"avg_us": round(ms_one * 1e3, 3),
+                               "GBps": round(mean_bytes / (ms_one * 1e-3) / 1e9, 1)}
     return layer, xs, routes
 
 

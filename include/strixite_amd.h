@@ -113,6 +113,29 @@ int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t
 int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A, const int32_t *ids,
                        const float *coef, const sx_qview *down, int64_t Ew, void *y, int act, uint32_t *expert_err,
                        sx_stream stream);
+/* ---- the whole verify-width MoE sublayer in one launch ----
+ * runtime/qwen4exp.cpp:1132-1163 below kGroupedMinTokens - the router projection (linear_bf16w, kernels/linear.hpp:19-24,
+ * or an FP32 weight), moe_router (moe_router.hpp:38-40), linear_q4_experts_gather_swiglu (linear_q4.hpp:55-56) and
+ * linear_q4_experts_combine (linear_q4.hpp:44-46) - as one kernel whose phases hand over through counters in `sync`
+ * instead of kernel boundaries; no reference counterpart as one call. wr: router weight [rows, d], FP32 (wr_act F32)
+ * or BF16 bits; logits [M, rows] FP32 are written; shared != 0: slot k is expert shared_id with coefficient
+ * sigmoid(logits[m, E]) (rows >= E + 1). ids, coef, h, h_sums, y, router_err, expert_err as sx_moe_verify_gate_up /
+ * sx_moe_verify_down. Shapes: those sx_moe_verify_supported takes, with d = 4096 and E <= 1024. sync: a device buffer
+ * of sx_moe_verify_layer_sync_bytes bytes, 16-byte aligned, zeroed once by the caller; one per stream: launches that
+ * overlap in time must not share it. The launch runs one block per compute unit and needs them resident together; a
+ * phase that waits more than 20 ms for another (another kernel holding compute units that long) gives up and sets
+ * expert_err {1, 0xFFFFFFFE, phase} instead of hanging. */
+int sx_moe_verify_layer_sync_bytes(size_t *bytes);
+/* Diagnostic: a device buffer of (compute units x 16) uint64 that later sx_moe_verify_layer launches (any thread) fill
+ * with each block's phase timestamps (s_memrealtime, 100 MHz): [0] start, [1] projection items done, [3] first gate_up
+ * weight loads issued (routing done), [4] gate_up done, [5] h complete, [6] h staged,
+ * [7] end. NULL turns it off (the default). No reference counterpart: the
+ * reference's tracing (common/trace.hpp) marks host-side launch ranges, which cannot show phases inside a launch. */
+int sx_moe_verify_layer_trace(uint64_t *buf);
+int sx_moe_verify_layer(const void *x, int64_t M, const void *wr, int wr_act, int64_t rows, int64_t E, int64_t k,
+                        int shared, int32_t shared_id, const sx_qview *gate_up, const sx_qview *down, int64_t Ew,
+                        float *logits, int32_t *ids, float *coef, void *h, float *h_sums, void *y, int act,
+                        uint32_t *router_err, uint32_t *expert_err, void *sync, sx_stream stream);
 /* y [M, A, N] (linear_q4_experts_gather_grouped, moe_grouped.hpp:53-55). */
 int sx_linear_q4_experts_gather_grouped(const void *x, const sx_qview *w, int64_t E, const void *ws, size_t ws_bytes,
                                         int64_t M, int64_t A, void *y, int act, int math, sx_stream stream);

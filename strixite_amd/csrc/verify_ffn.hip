@@ -24,6 +24,10 @@
 #include "route_impl.hpp"
 #include "verify_ffn.hpp"
 
+#include <atomic>
+#include <mutex>
+#include <unordered_map>
+
 namespace sx::vf {
 namespace {
 
@@ -99,20 +103,124 @@ __device__ void build_units(Routes &R, uint32_t *emask, int32_t id, int S, int A
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Cross-block hand-offs of the one-launch layer (layer_kernel below). Its blocks pass the router logits, h and the
+// h sums to each other through memory while the launch runs, across XCDs whose L2 caches are not coherent with each
+// other: those values are written and read with agent-scope accesses (sc1: written through to, and read from, the
+// level all XCDs share), and a block counts its contribution only after its own stores have completed.
+__device__ __forceinline__ void store_agent(uint16_t *p, uint16_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_agent(const uint32_t *p) {
+    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_agent64(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes at byte offset off of an array of `bytes` bytes, agent scope (a buffer load with sc1).
+__device__ __forceinline__ uint4 load16_agent(const void *base, uint32_t bytes, uint32_t off) {
+    const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)off, 0, 16 /* sc1 */);
+    return uint4{v[0], v[1], v[2], v[3]};
+}
+
+// The gate_up phase's work queue of a block: blocks 8j .. 8j + 7 (one on each XCD under the round-robin dispatch)
+// share queue j mod kQueues, so every queue is served by the same mix of XCDs and the queues drain together.
+__device__ __forceinline__ int queue_of(int block) { return (block >> 3) % kQueues; }
+constexpr int kDeadClaim = 1 << 24;  // a claim past every queue (the block's work is done)
+
+// One claim from a work counter by the calling lane. The zero offset comes from asm so the compiler cannot see
+// that every lane names one address: it would otherwise merge the lanes' atomics into one and read its result out
+// at once (readfirstlane), which waits for every load in flight; kept per lane, the wait lands where the result is
+// used, at the end of the round.
+__device__ __forceinline__ uint32_t claim_one(uint32_t *ctr) {
+    uint32_t z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return atomicAdd(ctr + z, 1u);
+}
+
+// The one-launch layer's hand-off flags (LayerSync in verify_ffn.hpp): block b stores the launch's epoch into its
+// slot of a phase once its part of that phase is complete (its own stores done), and a block that needs the phase
+// complete waits until every slot holds the epoch. No counter is shared, so no block ever queues behind another's
+// atomic; the host numbers the launches, so nothing needs resetting between them.
+constexpr uint64_t kWaitTicks = 2000000;           // 20 ms of the 100 MHz s_memrealtime clock
+constexpr uint32_t kWaitTimeoutCode = 0xFFFFFFFEu;  // expert_err word 1 after a wait gave up (word 2: the phase)
+
+// Every thread's own stores are complete, then thread 0 publishes the block's flag.
+__device__ __forceinline__ void block_publish(uint32_t *slot, uint32_t epoch) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(slot, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave 0 waits until flags[0 .. n) all hold epoch (n <= kMaxBlocks), or gives up after kWaitTicks and reports it;
+// the block learns the outcome through `flag` (LDS) after an LDS-only barrier (the loads already in flight, such
+// as the next weights, stay in flight). Every access after it comes after the wait.
+__device__ bool block_wait(const uint32_t *flags, int n, uint32_t epoch, uint32_t phase, uint32_t *err, int *flag) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        int ok = 1;
+        for (;;) {
+            bool mine = true;
+            for (int i = lane; i < n; i += 64) mine &= load_agent(flags + i) == epoch;
+            if (__ballot(!mine) == 0) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) {
+                ok = 0;
+                if (lane == 0) flag_error(err, kWaitTimeoutCode, phase);
+                break;
+            }
+        }
+        if (lane == 0) *flag = ok;
+    }
+    lds_barrier();
+    return __builtin_amdgcn_readfirstlane(*flag) != 0;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // gate_up + SwiGLU. A block takes an equal run of the (expert, 16-feature tile) items (to within one item of every
 // other block); its 8 waves split K Q ways (Q = K / 512: four spans a wave) and take 8 / Q items a round, so every
 // wave of the grid streams the same bytes: 8 loads a round (4 spans x gate, up), one round in flight. The Q partial
 // tiles of an item are summed in LDS after a barrier (Q > 1), in K order, and the item's SwiGLU rows are stored by
 // the Q waves that made them, a quarter-tile or less each. A wave's four spans of the M activation rows sit in its
-// registers as MFMA A operands (code order) for the whole kernel, with their span sums. LDS (static): the partial
-// tiles of two rounds, the routing.
-template <int NV, int Q>
-__global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
-    constexpr int P = kWaves / Q;  // items a round
-    __shared__ __attribute__((aligned(16))) float red[2][kWaves][2][4][64];  // [round & 1][wave][gate, up][v][lane]
-    __shared__ Routes R;
-    __shared__ __attribute__((aligned(16))) uint32_t emask[kMaxExperts];
+// registers as MFMA A operands (code order) for the whole kernel, with their span sums.
+//
+// FUSED (the one-launch layer): the logits come from the projection phase (agent-scope loads of the tagged pairs),
+// h and its sums are stored at agent scope for the down phase of every block, and the items come from one of
+// kQueues work queues (contiguous runs of the items, each shared by blocks spread over every XCD) one round at a
+// time, claimed two rounds ahead: a block that streams faster takes more rounds, so the blocks finish within about
+// a round of each other however unevenly the memory system serves them.
+struct GuLds {
+    float red[2][kWaves][2][4][64];  // [round & 1][wave][gate, up][v][lane]
+};
 
+struct DnLds {
+    alignas(16) uint16_t hs[kHsElems];
+    alignas(16) float hsum[kMaxSlots * kMaxSpansDn];
+    alignas(16) uint16_t zero_block[kZeroBytes / 2];
+    alignas(16) float red[kWaves][16][16];
+};
+
+struct FusedSched {
+    LayerSync *sync;
+    uint32_t *queue;         // this block's work counter (this launch's set)
+    int *rnd;                // LDS [4]: the claim (index into the block's queue) of round gr, slot gr & 3
+    const uint64_t *tagged;  // the projection's logits as (epoch << 32 | value bits) [M, ld]
+    uint32_t epoch;
+    uint64_t *trace;  // nullable: this block's stamp slots
+    int *flag;        // LDS scratch of block_wait
+};
+
+template <int NV, int Q, bool FUSED>
+__device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Routes &R, uint32_t *emask,
+                                            const FusedSched &fs) {
+    constexpr int P = kWaves / Q;  // items a round
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ip = wave / Q, kq = wave % Q;  // item lane, K slice (spans 4 kq .. 4 kq + 3)
@@ -124,10 +232,43 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
     // operand (span so, MFMA t) of lane (n16, g) = x[n16][128 (4 kq + so) + 32 g + 8 t ..+ 7] in code order
     const float *row0 = p.logits + (int64_t)min(wave, M - 1) * p.ld, *row1 = p.logits + (int64_t)min(wave + kWaves, M - 1) * p.ld;
     float v0[NV], v1[NV];
-    routing::load_logits<NV>([&](int e) { return row0[e]; }, p.E, v0);
-    routing::load_logits<NV>([&](int e) { return row1[e]; }, p.E, v1);
-    const float sl0 = p.shared_logit ? p.shared_logit[(int64_t)min(wave, M - 1) * p.shared_ld] : 0.f;
-    const float sl1 = p.shared_logit ? p.shared_logit[(int64_t)min(wave + kWaves, M - 1) * p.shared_ld] : 0.f;
+    float sl0 = 0.f, sl1 = 0.f;
+    if constexpr (FUSED) {
+        // the logits as the projection phase published them: (epoch, value) pairs, re-read until every one this wave
+        // needs carries this launch's epoch (or the wait gives up: error word, stale routing)
+        const uint64_t *t0 = fs.tagged + (int64_t)min(wave, M - 1) * p.ld;
+        const uint64_t *t1 = fs.tagged + (int64_t)min(wave + kWaves, M - 1) * p.ld;
+        const int ecol = p.shared_logit ? p.E : p.E - 1;  // the shared gate's column, or a routed one again
+        const uint64_t start = __builtin_amdgcn_s_memrealtime();
+        for (;;) {
+            bool fresh = true;
+            uint64_t a[NV], c[NV];
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int e = min((int)(threadIdx.x & 63) + 64 * j, p.E - 1);
+                a[j] = load_agent64(t0 + e), c[j] = load_agent64(t1 + e);
+            }
+            const uint64_t sa = load_agent64(t0 + ecol), sc = load_agent64(t1 + ecol);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                fresh &= (uint32_t)(a[j] >> 32) == fs.epoch && (uint32_t)(c[j] >> 32) == fs.epoch;
+                v0[j] = __uint_as_float((uint32_t)a[j]), v1[j] = __uint_as_float((uint32_t)c[j]);
+            }
+            fresh &= (uint32_t)(sa >> 32) == fs.epoch && (uint32_t)(sc >> 32) == fs.epoch;
+            sl0 = __uint_as_float((uint32_t)sa), sl1 = __uint_as_float((uint32_t)sc);
+            if (__ballot(!fresh) == 0) break;
+            if (__builtin_amdgcn_s_memrealtime() - start > kWaitTicks) {
+                if ((threadIdx.x & 63) == 0) flag_error(p.expert_err, kWaitTimeoutCode, 1);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    } else {
+        routing::load_logits<NV>([&](int e) { return row0[e]; }, p.E, v0);
+        routing::load_logits<NV>([&](int e) { return row1[e]; }, p.E, v1);
+        sl0 = p.shared_logit ? p.shared_logit[(int64_t)min(wave, M - 1) * p.shared_ld] : 0.f;
+        sl1 = p.shared_logit ? p.shared_logit[(int64_t)min(wave + kWaves, M - 1) * p.shared_ld] : 0.f;
+    }
     uint4 xr[4][4];
     {
         const uint16_t *xrow = p.x + (int64_t)min(n16, M - 1) * K + (int64_t)kq * 4 * kSpan + g * 32;
@@ -164,15 +305,25 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
         }
     }
 
-    // 3. this block's items [b0, b1) of U x T16 (expert-major), in rounds of P
+    // 3. the items of U x T16 (expert-major). Standalone: this block's run [b0, b1) in rounds of P. FUSED: rounds of
+    // one item (Q = 8) claimed from the queue [b0, b1) of this block (fs.rnd[gr & 3] = the claim of round gr)
     const int T16 = (int)((Nrows + 15) / 16);
     const int64_t F = (int64_t)U * T16;
-    const int b0 = (int)(blockIdx.x * F / gridDim.x), b1 = (int)((blockIdx.x + 1) * F / gridDim.x);
-    const int groups = (b1 - b0 + P - 1) / P;  // rounds (block-uniform)
-    if (groups <= 0) return;
+    const int part = FUSED ? queue_of(blockIdx.x) : (int)blockIdx.x, parts = FUSED ? kQueues : (int)gridDim.x;
+    const int b0 = (int)(part * F / parts), b1 = (int)((part + 1) * F / parts);
+    const int groups = FUSED ? 0 : (b1 - b0 + P - 1) / P;  // rounds (block-uniform; standalone)
+    auto live = [&](int gr) -> bool {
+        if constexpr (FUSED) return b0 + __builtin_amdgcn_readfirstlane(fs.rnd[gr & 3]) < b1;
+        else return gr < groups;
+    };
+    auto round_base = [&](int gr) -> int {
+        if constexpr (FUSED) return b0 + fs.rnd[gr & 3];
+        else return b0 + gr * P;
+    };
+    if (!live(0)) return;
 
-    // 4. weight ring: round r = the slice kq of item b0 + r P + ip (clamped into the run: a clamped round loads a
-    // valid tile and stores nothing); gate and up alternate, scale / min windows of the 4 spans
+    // 4. weight ring: round r = the slice kq of item round_base(r) + ip (clamped into the items: a clamped round
+    // loads a valid tile and stores nothing); gate and up alternate, scale / min windows of the 4 spans
     constexpr int NW = 2;
     const int64_t up_q = Nrows * rowbytes, up_g = Nrows * ngroups;
     uint4 ring[kRing][kPrefetch];
@@ -181,7 +332,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
     const uint8_t *iq = p.q;
     const uint16_t *is_ = p.scale, *im = p.minv;
     auto iplace = [&]() {
-        const int item = min(b0 + ii * P + ip, b1 - 1);
+        const int item = min(round_base(ii) + ip, b1 - 1);
         const int u = item / T16, tile = item - u * T16;
         const int64_t n = (int64_t)tile * 16 + n16, nn = n < Nrows ? n : Nrows - 1;
         const int64_t row = (int64_t)R.u_exp[u] * p.N + nn;
@@ -214,6 +365,9 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
         for (int s = 0; s < kPrefetch; ++s) issue_slot(ring[r], s);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FUSED) {
+        if (fs.trace && tid == 0) fs.trace[3] = __builtin_amdgcn_s_memrealtime();
+    }
 
     // 5. the A operands (zero rows past M) and the span sums of the tokens of this lane's D rows 4 g + v
     bf16x8 aop[4][4];
@@ -258,10 +412,16 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
             const float gv = as_bf16(gate[j]), uv = as_bf16(up[j]);
             const uint32_t hb = f32_to_bf16(as_bf16(silu(gv)) * uv);
             const int slot = on ? R.slot_tab[u][r] : 0;
-            if (on && n_in) p.h[(int64_t)slot * Nrows + n] = (uint16_t)hb;
+            if (on && n_in) {
+                if constexpr (FUSED) store_agent(p.h + (int64_t)slot * Nrows + n, (uint16_t)hb);
+                else p.h[(int64_t)slot * Nrows + n] = (uint16_t)hb;
+            }
             if (p.h_sums) {
                 const float ts = qmm::detail::group_sum_c<16>(n_in ? bf16_to_f32(hb) : 0.f);
-                if (on && n16 == 0) p.h_sums[(int64_t)slot * T16 + tile] = ts;
+                if (on && n16 == 0) {
+                    if constexpr (FUSED) store_agent(p.h_sums + (int64_t)slot * T16 + tile, ts);
+                    else p.h_sums[(int64_t)slot * T16 + tile] = ts;
+                }
             }
         }
     };
@@ -269,10 +429,14 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
     // 6. consume: A rows = tokens (lane row n16), D rows 4g .. 4g + 3 = tokens, columns = the 16 features
     auto consume = [&](int gr, auto slot_tag) __attribute__((always_inline)) {
         constexpr int RS = decltype(slot_tag)::value;
+        int claimed = 0;
+        if constexpr (FUSED) {  // round gr + 2, claimed while this one streams (written to LDS before the barrier)
+            if (tid == 0) claimed = live(gr + 1) ? (int)claim_one(fs.queue) : kDeadClaim;
+        }
         uint2 sw[NW], mw[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) sw[w] = sw_n[RS][w], mw[w] = mw_n[RS][w];
-        if (gr + kRing < groups) advance_issue();
+        if (FUSED || gr + kRing < groups) advance_issue();
         issue_window(sw_n[RS], mw_n[RS]);
         float acc[NW][4] = {};
 #pragma unroll
@@ -295,16 +459,19 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
         }
 #pragma unroll
         for (int s = kPrefetch - kLag; s < kPrefetch; ++s) issue_slot(ring[RS], s);
-        if (gr >= groups) return;  // the phantom round
-        const int item = b0 + gr * P + ip;
+        if (!FUSED && gr >= groups) return;  // the phantom round
+        const int item = round_base(gr) + ip;
         if constexpr (Q == 1) {
             if (item < b1) epilogue(item, acc[0], acc[1]);
         } else {
-            float(&mine)[2][4][64] = red[gr & 1][wave];
+            float(&mine)[2][4][64] = L.red[gr & 1][wave];
 #pragma unroll
             for (int w = 0; w < NW; ++w)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) mine[w][v][lane] = acc[w][v];
+            if constexpr (FUSED) {
+                if (tid == 0) fs.rnd[(gr + 2) & 3] = claimed;
+            }
             // every wave's partial tile of this round is in LDS (the loads in flight stay in flight); the next
             // write to this half of red comes after the next round's barrier, when these reads are done
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -312,7 +479,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
                 float gate[VS] = {}, up[VS] = {};
 #pragma unroll
                 for (int qq = 0; qq < Q; ++qq) {  // K order
-                    const float(&part)[2][4][64] = red[gr & 1][ip * Q + qq];
+                    const float(&part)[2][4][64] = L.red[gr & 1][ip * Q + qq];
 #pragma unroll
                     for (int j = 0; j < VS; ++j) gate[j] += part[0][vb + j][lane], up[j] += part[1][vb + j][lane];
                 }
@@ -320,63 +487,92 @@ __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
             }
         }
     };
-    // Runs of kRing rounds, all issuing their loads (an odd count ends with a phantom round that re-loads the last
-    // one and stops after its MFMAs): a consume whose loads were conditional would merge two versions of the ring
-    // registers, and the copies at such a merge wait for every outstanding load.
-    for (int gr = 0; gr < groups; gr += kRing)
-        [&]<int... RS>(std::integer_sequence<int, RS...>) {
-            (consume(gr + RS, std::integral_constant<int, RS>{}), ...);
-        }(std::make_integer_sequence<int, kRing>{});
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave exits
+    if constexpr (FUSED) {
+        static_assert(!FUSED || (Q > 1 && kRing == 1), "the claims are published at the round's barrier");
+        // a live round always issues the next one's loads (clamped when that one is dead): one path for the ring
+        for (int gr = 0;; ++gr) {
+            consume(gr, std::integral_constant<int, 0>{});
+            if (!live(gr + 1)) break;
+        }
+    } else {
+        // Runs of kRing rounds, all issuing their loads (an odd count ends with a phantom round that re-loads the
+        // last one and stops after its MFMAs): a consume whose loads were conditional would merge two versions of
+        // the ring registers, and the copies at such a merge wait for every outstanding load.
+        for (int gr = 0; gr < groups; gr += kRing)
+            [&]<int... RS>(std::integer_sequence<int, RS...>) {
+                (consume(gr + RS, std::integral_constant<int, RS>{}), ...);
+            }(std::make_integer_sequence<int, kRing>{});
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave moves on
+}
+
+template <int NV, int Q>
+__global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
+    __shared__ __attribute__((aligned(16))) GuLds L;
+    __shared__ Routes R;
+    __shared__ __attribute__((aligned(16))) uint32_t emask[kMaxExperts];
+    gate_up_body<NV, Q, false>(p, L, R, emask, FusedSched{});
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// down + combine. LDS (static): the S slot rows of h [S][K + 8] BF16 (code order), span sums [S][K / 128], a zero
-// block, the waves' partial sums [8][16 tokens][16 rows].
-template <int NB, bool SUMS>
-__global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t hs[kHsElems];
-    __shared__ __attribute__((aligned(16))) float hsum[kMaxSlots * kMaxSpansDn];
-    __shared__ __attribute__((aligned(16))) uint16_t zero_block[kZeroBytes / 2];
-    __shared__ __attribute__((aligned(16))) float red[kWaves][16][16];
-    __shared__ Routes R;
-    __shared__ __attribute__((aligned(16))) uint32_t emask[kMaxExperts];
-
+// down + combine. A block owns 16 output rows for all tokens; LDS: the S slot rows of h [S][K + 8] BF16 (code
+// order), span sums [S][K / 128], a zero block, the waves' partial sums [8][16 tokens][16 rows].
+//
+// Standalone (down_kernel): the routing and h come from memory (written by the gate_up launch). FUSED: the routing
+// is the block's own (LDS, from the gate_up phase), h and its sums are staged once per block after the gate_up
+// phase's counter is complete (agent-scope loads; this row block's first weight loads are already in flight), and
+// the block may take several row blocks.
+template <int NB, bool SUMS, bool FUSED>
+__device__ __forceinline__ void down_body(const DownParams &p, DnLds &L, Routes &R, uint32_t *emask, int64_t n0,
+                                          bool stage_h, const FusedSched &fs, bool &ok) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = p.M, A = p.A, S = M * A, Ew = p.Ew;
     const int64_t K = p.K, ldh = K + 8, N = p.N;
     const int nspan = (int)(K / kSpan), chunks8 = (int)(K / 8), lg_chunks = __builtin_ctz((unsigned)chunks8);
     const int n_items_x = S * chunks8;
-    const int64_t n0 = (int64_t)blockIdx.x * 16;
 
-    // the routing first, then the rows of h: the grouping waits for the ids only
-    int32_t my_id;
-    float my_coef;
-    my_id = p.ids[min(lane, S - 1)], my_coef = p.coef[min(lane, S - 1)];  // every wave: no branch around loads
     constexpr int kSumLoads = SUMS ? (kMaxSlots * kMaxSpansDn + kThreads - 1) / kThreads : 0;
     float4 tsum[kSumLoads > 0 ? kSumLoads : 1][2];  // SUMS: the 8 tile sums of (slot, span) i = b * kThreads + tid
-    if constexpr (SUMS) {
-        const int tiles = (int)(K / 16);
-#pragma unroll
-        for (int b = 0; b < kSumLoads; ++b) {
-            const int i = min(b * kThreads + tid, S * nspan - 1), r = i / nspan, sp = i - r * nspan;
-            const float4 *src = reinterpret_cast<const float4 *>(p.h_sums + (int64_t)r * tiles + sp * 8);
-            tsum[b][0] = src[0], tsum[b][1] = src[1];
-        }
-    }
     uint4 raw[NB];
+    auto load_h = [&]() __attribute__((always_inline)) {
+        const int tiles = (int)(K / 16);
+        if constexpr (SUMS) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int i = min(b * kThreads + tid, n_items_x - 1);
-        raw[b] = *reinterpret_cast<const uint4 *>(p.h + (int64_t)(i >> lg_chunks) * K + (int64_t)(i & (chunks8 - 1)) * 8);
+            for (int b = 0; b < kSumLoads; ++b) {
+                const int i = min(b * kThreads + tid, S * nspan - 1), r = i / nspan, sp = i - r * nspan;
+                if constexpr (FUSED) {
+                    const uint32_t off = (uint32_t)(((int64_t)r * tiles + sp * 8) * 4);
+                    const uint4 a = load16_agent(p.h_sums, (uint32_t)(S * tiles * 4), off);
+                    const uint4 c = load16_agent(p.h_sums, (uint32_t)(S * tiles * 4), off + 16);
+                    tsum[b][0] = float4{__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z), __uint_as_float(a.w)};
+                    tsum[b][1] = float4{__uint_as_float(c.x), __uint_as_float(c.y), __uint_as_float(c.z), __uint_as_float(c.w)};
+                } else {
+                    const float4 *src = reinterpret_cast<const float4 *>(p.h_sums + (int64_t)r * tiles + sp * 8);
+                    tsum[b][0] = src[0], tsum[b][1] = src[1];
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int i = min(b * kThreads + tid, n_items_x - 1);
+            const int64_t e = (int64_t)(i >> lg_chunks) * K + (int64_t)(i & (chunks8 - 1)) * 8;
+            if constexpr (FUSED) raw[b] = load16_agent(p.h, (uint32_t)(S * K * 2), (uint32_t)(e * 2));
+            else raw[b] = *reinterpret_cast<const uint4 *>(p.h + e);
+        }
+    };
+    if constexpr (!FUSED) {
+        // the routing first, then the rows of h: the grouping waits for the ids only
+        const int32_t my_id = p.ids[min(lane, S - 1)];  // every wave: no branch around loads
+        const float my_coef = p.coef[min(lane, S - 1)];
+        load_h();
+        R.ids[lane] = my_id, R.coef[lane] = my_coef;  // every wave the same values (unconditional: nothing sinks the loads)
+        for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(L.zero_block)[i] = 0u;
+        build_units(R, emask, my_id, S, A, Ew);  // its closing barrier also covers ids, coef and the zero block
     }
-    R.ids[lane] = my_id, R.coef[lane] = my_coef;  // every wave the same values (unconditional: nothing sinks the loads)
-    for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(zero_block)[i] = 0u;
-    build_units(R, emask, my_id, S, A, Ew);  // its closing barrier also covers ids, coef and the zero block
     const int U = __builtin_amdgcn_readfirstlane(R.U);
     const uint64_t bad_slots = R.bad_slots;
-    if (blockIdx.x == 0 && bad_slots && tid == 0) {
+    if (!FUSED && blockIdx.x == 0 && bad_slots && tid == 0) {  // (FUSED: reported by the gate_up phase)
         const int s = __builtin_ctzll(bad_slots);
         flag_error(p.expert_err, (uint32_t)R.ids[s], (uint32_t)s);
     }
@@ -423,42 +619,53 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    if constexpr (SUMS) {  // h in code order; span sums = the 8 tile sums in tile order
+    if (!FUSED || stage_h) {
+        if constexpr (FUSED) {  // h is complete once every block has published its gate_up part
+            ok = block_wait(fs.sync->done_b, (int)gridDim.x, fs.epoch, 2, p.expert_err, fs.flag);
+            if (fs.trace && tid == 0) fs.trace[5] = __builtin_amdgcn_s_memrealtime();
+            load_h();
+            for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(L.zero_block)[i] = 0u;
+        }
+        if constexpr (SUMS) {  // h in code order; span sums = the 8 tile sums in tile order
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int i = b * kThreads + tid;
-            if (i < n_items_x) {
-                const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
-                const uint4 w = raw[b];
-                *reinterpret_cast<uint4 *>(hs + r * ldh + (int64_t)c8 * 8) =
-                    uint4{__builtin_amdgcn_perm(w.z, w.x, 0x05040100u), __builtin_amdgcn_perm(w.z, w.x, 0x07060302u),
-                          __builtin_amdgcn_perm(w.w, w.y, 0x05040100u), __builtin_amdgcn_perm(w.w, w.y, 0x07060302u)};
+            for (int b = 0; b < NB; ++b) {
+                const int i = b * kThreads + tid;
+                if (i < n_items_x) {
+                    const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
+                    const uint4 w = raw[b];
+                    *reinterpret_cast<uint4 *>(L.hs + r * ldh + (int64_t)c8 * 8) =
+                        uint4{__builtin_amdgcn_perm(w.z, w.x, 0x05040100u), __builtin_amdgcn_perm(w.z, w.x, 0x07060302u),
+                              __builtin_amdgcn_perm(w.w, w.y, 0x05040100u), __builtin_amdgcn_perm(w.w, w.y, 0x07060302u)};
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < kSumLoads; ++b) {
+                const int i = b * kThreads + tid;
+                if (i < S * nspan) {
+                    const float4 a = tsum[b][0], c = tsum[b][1];
+                    L.hsum[i] = ((((((a.x + a.y) + a.z) + a.w) + c.x) + c.y) + c.z) + c.w;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int i = b * kThreads + tid;
+                if (i < n_items_x) {
+                    const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
+                    uint4 planes[1];
+                    float sum;
+                    qmm::detail::chunk_planes<4, 1, uint16_t>(raw[b], planes, sum);
+                    *reinterpret_cast<uint4 *>(L.hs + r * ldh + (int64_t)c8 * 8) = planes[0];
+                    sum = qmm::detail::group_sum_c<16>(sum);
+                    if ((c8 & 15) == 0) L.hsum[r * nspan + (c8 >> 4)] = sum;
+                }
             }
         }
-#pragma unroll
-        for (int b = 0; b < kSumLoads; ++b) {
-            const int i = b * kThreads + tid;
-            if (i < S * nspan) {
-                const float4 a = tsum[b][0], c = tsum[b][1];
-                hsum[i] = ((((((a.x + a.y) + a.z) + a.w) + c.x) + c.y) + c.z) + c.w;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const int i = b * kThreads + tid;
-            if (i < n_items_x) {
-                const int r = i >> lg_chunks, c8 = i & (chunks8 - 1);
-                uint4 planes[1];
-                float sum;
-                qmm::detail::chunk_planes<4, 1, uint16_t>(raw[b], planes, sum);
-                *reinterpret_cast<uint4 *>(hs + r * ldh + (int64_t)c8 * 8) = planes[0];
-                sum = qmm::detail::group_sum_c<16>(sum);
-                if ((c8 & 15) == 0) hsum[r * nspan + (c8 >> 4)] = sum;
-            }
+        lds_barrier();  // the ring's weight loads stay in flight
+        if constexpr (FUSED) {
+            if (fs.trace && tid == 0) fs.trace[6] = __builtin_amdgcn_s_memrealtime();
         }
     }
-    lds_barrier();  // the ring's weight loads stay in flight
 
     // consume: per item, A row n16 = token n16's slot of the unit's expert (or zeros); D rows 4g + v = tokens
     float yacc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -470,7 +677,7 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
         const int item = max(min(i0 + gr, F - 1), 0);
         const int u = item / C, c0 = (item - u * C) * SPG;
         const int sa = R.slot_tab[u][n16];
-        const uint16_t *ab = sa >= 0 ? hs + sa * ldh + g * 32 + c0 * kSpan : zero_block;
+        const uint16_t *ab = sa >= 0 ? L.hs + sa * ldh + g * 32 + c0 * kSpan : L.zero_block;
         const int a_step = sa >= 0 ? kSpan : 0;
         int sv[4];
 #pragma unroll
@@ -495,7 +702,7 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
             const float cm = fmaf(-128.f, s_, m_);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float xv = sv[v] >= 0 ? hsum[sv[v] * nspan + c0 + s] : 0.f;
+                const float xv = sv[v] >= 0 ? L.hsum[sv[v] * nspan + c0 + s] : 0.f;
                 acc[v] = fmaf(s_, D[v], fmaf(cm, xv, acc[v]));
             }
         }
@@ -517,14 +724,14 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
 
     // the waves' sums in wave order; tokens with an invalid slot get NaN rows (the combine's rule)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[wave][4 * g + v][n16] = yacc[v];
+    for (int v = 0; v < 4; ++v) L.red[wave][4 * g + v][n16] = yacc[v];
     __syncthreads();
     if (tid < M * 16) {
         const int m = tid >> 4, c = tid & 15;
         const int64_t n = n0 + c;
         float y = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) y += red[w][m][c];
+        for (int w = 0; w < kWaves; ++w) y += L.red[w][m][c];
         bool bad = false;
         for (int a = 0; a < A; ++a) bad |= (bad_slots >> (m * A + a)) & 1ull;
         if (bad) y = qnan();
@@ -533,6 +740,150 @@ __global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
             else static_cast<uint16_t *>(p.y)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16(y);
         }
     }
+    if constexpr (FUSED) __syncthreads();  // red is rewritten by the next row block
+}
+
+template <int NB, bool SUMS>
+__global__ void __launch_bounds__(kThreads) down_kernel(DownParams p) {
+    __shared__ __attribute__((aligned(16))) DnLds L;
+    __shared__ Routes R;
+    __shared__ __attribute__((aligned(16))) uint32_t emask[kMaxExperts];
+    bool ok = true;
+    down_body<NB, SUMS, false>(p, L, R, emask, (int64_t)blockIdx.x * 16, true, FusedSched{}, ok);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// The router projection as the one-launch layer's first phase: block b projects weight rows [a R / PA, (a + 1) R / PA)
+// for a = b, b + G, ... (at most kProjRows rows each); each thread owns 8-column chunks of those rows (every 512th),
+// issues its weight and activation loads before any use, and the per-(row, token) sums meet in a wave sum and
+// across the waves in LDS in a fixed order. Each logit goes to the output and, tagged with the launch's epoch as one
+// 64-bit agent-scope store, to the pairs the routing of every block polls.
+constexpr int kProjRows = 4;
+
+struct ProjLds {
+    float part[kWaves][kProjRows * kMaxTokens];
+};
+
+template <typename TW, int MT>
+__device__ __forceinline__ void project_item(const LayerParams &lp, ProjLds &L, int r0, int nr) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int M = lp.gu.M;
+    const int64_t K = lp.gu.K, K8 = K / 8;
+    const TW *W = static_cast<const TW *>(lp.wr);
+    float acc[kProjRows][MT];
+#pragma unroll
+    for (int r = 0; r < kProjRows; ++r)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[r][t] = 0.f;
+    for (int64_t c = tid; c < K8; c += kThreads) {
+        float wv[kProjRows][8];
+#pragma unroll
+        for (int r = 0; r < kProjRows; ++r) {
+            const TW *wr = W + (int64_t)(r0 + min(r, nr - 1)) * K + c * 8;
+            if constexpr (sizeof(TW) == 4) {
+                const float4 a = reinterpret_cast<const float4 *>(wr)[0], b = reinterpret_cast<const float4 *>(wr)[1];
+                wv[r][0] = a.x, wv[r][1] = a.y, wv[r][2] = a.z, wv[r][3] = a.w;
+                wv[r][4] = b.x, wv[r][5] = b.y, wv[r][6] = b.z, wv[r][7] = b.w;
+            } else {
+                qmm::detail::unpack8(*reinterpret_cast<const uint4 *>(wr), wv[r]);
+            }
+        }
+        uint4 xr[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) xr[t] = *reinterpret_cast<const uint4 *>(lp.gu.x + (int64_t)min(t, M - 1) * K + c * 8);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            if (t < M) {  // uniform
+                float xv[8];
+                qmm::detail::unpack8(xr[t], xv);
+#pragma unroll
+                for (int r = 0; r < kProjRows; ++r)
+                    if (r < nr)  // uniform
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[r][t] = fmaf(xv[e], wv[r][e], acc[r][t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kProjRows; ++r)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            if (r < nr && t < M) {  // uniform
+                const float s = routing::wave_sum_f32(acc[r][t]);
+                if (lane == 0) L.part[wave][r * kMaxTokens + t] = s;
+            }
+        }
+    lds_barrier();
+    if (tid < nr * kMaxTokens) {
+        const int r = tid / kMaxTokens, t = tid % kMaxTokens;
+        if (t < M) {
+            float y = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) y += L.part[w][tid];
+            const int64_t i = (int64_t)t * lp.ld + r0 + r;
+            lp.logits[i] = y;
+            __hip_atomic_store(lp.tagged + i, ((uint64_t)lp.epoch << 32) | __float_as_uint(y), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    lds_barrier();  // part is rewritten by the next item (an LDS-only barrier: the stores complete in the background)
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// The whole verify-width MoE sublayer in one launch: router projection -> routing (each block its own copy) ->
+// gate_up + SwiGLU -> down + combine, the phases handed over through per-block flags (LayerSync) rather than kernel
+// boundaries: no phase waits for a launch, and the down phase's first weight loads go out while the last gate_up rounds
+// finish. Each block's share of every phase is fixed (the shares of the two-launch kernels), so the launch relies on
+// all its blocks being resident together (one 512-thread block a compute unit, as the launch sizes it); a wait that
+// does not complete in 20 ms - another kernel holding compute units for that long - gives up with an error word
+// instead of hanging.
+union LayerPool {  // the phases' LDS, one after the other
+    ProjLds proj;
+    GuLds gu;
+    DnLds dn;
+};
+
+template <int NV, int Q, int NB, typename TW, int MT>
+__global__ void __launch_bounds__(kThreads) layer_kernel(LayerParams lp) {
+    __shared__ __attribute__((aligned(16))) LayerPool pool;
+    __shared__ Routes R;
+    __shared__ __attribute__((aligned(16))) uint32_t emask[kMaxExperts];
+    __shared__ int s_flag, s_rnd[4];
+    LayerSync *sync = lp.sync;
+    const int tid = threadIdx.x, G = (int)gridDim.x, b = (int)blockIdx.x;
+    uint64_t *trace = lp.trace ? lp.trace + (int64_t)b * kTraceSlots : nullptr;
+    auto stamp = [&](int i) {
+        if (trace && tid == 0) trace[i] = __builtin_amdgcn_s_memrealtime();
+    };
+    stamp(0);
+    uint32_t *queue = &sync->queues[lp.epoch & 1][queue_of(b)][0];
+    const FusedSched fs{sync, queue, s_rnd, lp.tagged, lp.epoch, trace, &s_flag};
+    if (tid == 0) {  // the first two gate_up rounds (claims do not depend on the routing)
+        s_rnd[0] = (int)atomicAdd(queue, 1u);
+        s_rnd[1] = (int)atomicAdd(queue, 1u);
+    }
+    if (b == 0 && tid < kQueues)  // the other set of counters, used by the next launch, starts from zero
+        __hip_atomic_store(&sync->queues[(lp.epoch + 1) & 1][tid][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // phase A: the router projection, rows [a R / PA, (a + 1) R / PA) for a = b, b + G, ... (at most kProjRows each)
+    const int rows = lp.rows, PA = max(G, (rows + kProjRows - 1) / kProjRows);
+    for (int a = b; a < PA; a += G) {
+        const int r0 = (int)((int64_t)a * rows / PA), r1 = (int)((int64_t)(a + 1) * rows / PA);
+        if (r1 > r0) project_item<TW, MT>(lp, pool.proj, r0, r1 - r0);
+    }
+    stamp(1);
+
+    // phase B: routing (each routing wave polls the tagged logits it needs) + gate_up + SwiGLU
+    bool ok = true;
+    gate_up_body<NV, Q, true>(lp.gu, pool.gu, R, emask, fs);
+    stamp(4);
+    block_publish(&sync->done_b[b], lp.epoch);
+
+    // phase C: down + combine, output rows [16 rb, 16 rb + 16) for rb = b, b + G, ...
+    const int nrb = (int)((lp.dn.N + 15) / 16);
+    for (int rb = b; rb < nrb && ok; rb += G) down_body<NB, true, true>(lp.dn, pool.dn, R, emask, (int64_t)rb * 16, rb == b, fs, ok);
+    stamp(7);
 }
 
 }  // namespace
@@ -564,6 +915,21 @@ hipError_t launch_down(const DownParams &p, hipStream_t stream) {
     if (nb <= 4) sums ? down_kernel<4, true><<<grid, kThreads, 0, stream>>>(p) : down_kernel<4, false><<<grid, kThreads, 0, stream>>>(p);
     else if (nb <= 8) sums ? down_kernel<8, true><<<grid, kThreads, 0, stream>>>(p) : down_kernel<8, false><<<grid, kThreads, 0, stream>>>(p);
     else sums ? down_kernel<16, true><<<grid, kThreads, 0, stream>>>(p) : down_kernel<16, false><<<grid, kThreads, 0, stream>>>(p);
+    return hipGetLastError();
+}
+
+hipError_t launch_layer(const LayerParams &p, bool wr_f32, int cus, hipStream_t stream) {
+    const dim3 grid((unsigned)cus);
+    auto go = [&](auto nv_tag, auto tw) {
+        if (p.gu.M <= 8) layer_kernel<decltype(nv_tag)::value, 8, 16, decltype(tw), 8><<<grid, kThreads, 0, stream>>>(p);
+        else layer_kernel<decltype(nv_tag)::value, 8, 16, decltype(tw), 16><<<grid, kThreads, 0, stream>>>(p);
+    };
+    auto by_w = [&](auto nv_tag) {
+        if (wr_f32) go(nv_tag, float{});
+        else go(nv_tag, uint16_t{});
+    };
+    if (p.gu.E <= 512) by_w(std::integral_constant<int, 8>{});
+    else by_w(std::integral_constant<int, 16>{});
     return hipGetLastError();
 }
 
@@ -652,6 +1018,75 @@ int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A,
     p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = N, p.K = w->K, p.y = y, p.act = act;
     p.expert_err = expert_err;
     SX_HIP(vf::launch_down(p, stream_of(stream)), fn);
+    return SX_OK;
+}
+
+namespace {
+std::atomic<uint64_t *> g_layer_trace{nullptr};
+
+// The launch number of a sync buffer: 1, 2, ... (never 0, the value of a freshly zeroed buffer).
+uint32_t next_epoch(const void *sync) {
+    static std::mutex mu;
+    static std::unordered_map<const void *, uint32_t> epochs;
+    std::lock_guard<std::mutex> lock(mu);
+    uint32_t &e = epochs[sync];
+    if (++e == 0) ++e;
+    return e;
+}
+}
+
+int sx_moe_verify_layer_trace(uint64_t *buf) {
+    g_layer_trace.store(buf);
+    return SX_OK;
+}
+
+int sx_moe_verify_layer_sync_bytes(size_t *bytes) {
+    SX_CHECK(bytes != nullptr, "null output");
+    *bytes = sizeof(vf::LayerSync);
+    return SX_OK;
+}
+
+int sx_moe_verify_layer(const void *x, int64_t M, const void *wr, int wr_act, int64_t rows, int64_t E, int64_t k,
+                        int shared, int32_t shared_id, const sx_qview *gate_up, const sx_qview *down, int64_t Ew,
+                        float *logits, int32_t *ids, float *coef, void *h, float *h_sums, void *y, int act,
+                        uint32_t *router_err, uint32_t *expert_err, void *sync, sx_stream stream) {
+    const char *fn = "sx_moe_verify_layer";
+    SX_CHECK(x && wr && logits && ids && coef && h && h_sums && y && router_err && expert_err && sync, fn,
+             " null pointer");
+    const int64_t A = k + (shared ? 1 : 0);
+    if (int rc = check_gate_up(fn, M, A, E, k, Ew, gate_up, act)) return rc;
+    if (int rc = check_down(fn, M, A, Ew, down, act)) return rc;
+    const int64_t K = gate_up->K, I = gate_up->N / Ew / 2, d = down->N / Ew;
+    SX_CHECK(device_cus() <= vf::kMaxBlocks, fn, " more compute units than the sync buffer has slots");
+    SX_CHECK(K == 4096 && E <= 1024, fn, " the one-launch layer takes d = 4096 and E <= 1024 (d = ", K, ", E = ", E,
+             "); the two-launch FFN takes the others");
+    SX_CHECK(down->K == I && d == K, fn, " down [", d, ", ", down->K, "] does not match gate_up's I = ", I,
+             " and d = ", K);
+    SX_CHECK(wr_act == SX_ACT_F32 || wr_act == SX_ACT_BF16, fn, " router weight dtype ", wr_act);
+    SX_CHECK(rows >= E + (shared ? 1 : 0) && rows <= vf::kMaxRouterRows, fn, " router weight has ", rows, " rows for E = ", E,
+             shared ? " plus the shared gate" : "");
+    SX_CHECK(aligned(wr, 16) && aligned(x, 16) && aligned(h, 16) && aligned(h_sums, 16) && aligned(sync, 16), fn,
+             " x, the router weight, h, h_sums and sync must be 16-byte aligned");
+    SX_CHECK(apart(logits, M * rows * 4, x, M * K * 2) && apart(h, M * A * I * 2, x, M * K * 2) &&
+                 apart(y, M * d * 2, h, M * A * I * 2) && apart(y, M * d * 2, x, M * K * 2),
+             fn, " outputs overlap inputs");
+    vf::LayerParams lp{};
+    vf::GateUpParams &p = lp.gu;
+    p.x = static_cast<const uint16_t *>(x), p.M = (int)M, p.A = (int)A, p.k = (int)k, p.E = (int)E, p.Ew = (int)Ew;
+    p.logits = logits, p.ld = rows, p.shared_logit = shared ? logits + E : nullptr, p.shared_ld = rows;
+    p.shared_id = shared_id;
+    p.q = gate_up->q, p.scale = gate_up->scale, p.minv = gate_up->minv, p.N = gate_up->N / Ew, p.K = K;
+    p.ids = ids, p.coef = coef, p.h = static_cast<uint16_t *>(h), p.h_sums = h_sums;
+    p.router_err = router_err, p.expert_err = expert_err;
+    vf::DownParams &q = lp.dn;
+    q.h = p.h, q.h_sums = h_sums, q.M = (int)M, q.A = (int)A, q.Ew = (int)Ew, q.ids = ids, q.coef = coef;
+    q.q = down->q, q.scale = down->scale, q.minv = down->minv, q.N = d, q.K = I, q.y = y, q.act = act;
+    q.expert_err = expert_err;
+    lp.wr = wr, lp.rows = (int)rows, lp.logits = logits, lp.ld = rows, lp.sync = static_cast<vf::LayerSync *>(sync);
+    lp.trace = g_layer_trace.load();
+    lp.tagged = lp.sync->tagged;
+    lp.epoch = next_epoch(sync);
+    SX_HIP(vf::launch_layer(lp, wr_act == SX_ACT_F32, device_cus(), stream_of(stream)), fn);
     return SX_OK;
 }
 

@@ -43,7 +43,35 @@ struct DownParams {
     uint32_t *expert_err;
 };
 
+// The one-launch layer's shared state: block b stores the launch's epoch (numbered by the host, never 0) into its
+// slot of a phase when its part of the phase is done; the logits are published tagged with the epoch; the gate_up
+// work counters alternate between two sets by epoch parity. Zero before the first launch; nothing to reset after one.
+constexpr int kMaxBlocks = 1024;
+constexpr int kMaxRouterRows = 1040;  // router weight rows: E + 1 <= 1025
+constexpr int kQueues = 16;           // gate_up work queues
+struct LayerSync {
+    uint32_t queues[2][kQueues][32];  // gate_up round counters, one 128-byte line each; set epoch & 1 in use (the
+                                      // other one is zeroed during the launch for the next)
+    uint32_t done_b[kMaxBlocks];  // routing + gate_up + SwiGLU (h, h_sums) done
+    uint64_t tagged[kMaxTokens * kMaxRouterRows];  // the router logits as (epoch << 32 | value bits) [M, rows]
+};
+
+struct LayerParams {
+    GateUpParams gu;    // gu.logits = logits (written by the projection phase); gu.h_sums required
+    DownParams dn;      // dn.h = gu.h, dn.h_sums = gu.h_sums; ids / coef unused (the routing stays in LDS)
+    const void *wr;     // router weight [rows, K]: FP32 or BF16
+    int rows;
+    float *logits;      // [M, ld = rows]
+    int64_t ld;
+    LayerSync *sync;
+    uint64_t *tagged;   // = sync->tagged, [M, ld]
+    uint32_t epoch;
+    uint64_t *trace;    // nullable: per block, s_memrealtime stamps of its phase boundaries (kTraceSlots a block)
+};
+constexpr int kTraceSlots = 16;
+
 hipError_t launch_gate_up(const GateUpParams &p, int cus, hipStream_t stream);
 hipError_t launch_down(const DownParams &p, hipStream_t stream);
+hipError_t launch_layer(const LayerParams &p, bool wr_f32, int cus, hipStream_t stream);
 
 }  // namespace sx::vf

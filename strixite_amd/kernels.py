@@ -164,6 +164,38 @@ def verify_down(h, w, ids, coef, Ew, y=None, expert_err=None, h_sums=None, strea
     return y, expert_err
 
 
+def verify_layer_sync(device="cuda"):
+    """A zeroed sync buffer for verify_layer (one per stream; every launch leaves it zero)."""
+    n = ctypes.c_size_t()
+    check(lib().sx_moe_verify_layer_sync_bytes(ctypes.byref(n)))
+    return torch.zeros((n.value + 3) // 4, dtype=torch.int32, device=device)
+
+
+def verify_layer(x, Wr, gate_up, down, E, k, sync, shared=False, shared_id=0, Ew=None, logits=None, ids=None,
+                 coef=None, h=None, h_sums=None, y=None, router_err=None, expert_err=None, stream=None):
+    """The verify-width MoE sublayer in one launch: x [M, d] BF16, Wr [rows, d] FP32 or BF16 (raw bits as int16 or
+    torch.bfloat16) -> logits [M, rows], ids / coef [M, A], h [M, A, I], h_sums, y [M, d]."""
+    M, d = x.shape
+    rows = Wr.shape[0]
+    Ew = E if Ew is None else Ew
+    A = k + (1 if shared else 0)
+    I = gate_up.N // Ew // 2
+    dev = x.device
+    wr_act = ACT_F32 if Wr.dtype == torch.float32 else ACT_BF16
+    logits = torch.empty((M, rows), dtype=torch.float32, device=dev) if logits is None else logits
+    ids = torch.empty((M, A), dtype=torch.int32, device=dev) if ids is None else ids
+    coef = torch.empty((M, A), dtype=torch.float32, device=dev) if coef is None else coef
+    h = torch.empty((M, A, I), dtype=x.dtype, device=dev) if h is None else h
+    h_sums = torch.empty((M * A, (I + 15) // 16), dtype=torch.float32, device=dev) if h_sums is None else h_sums
+    y = torch.empty((M, down.N // Ew), dtype=x.dtype, device=dev) if y is None else y
+    router_err = _err(dev) if router_err is None else router_err
+    expert_err = _err(dev) if expert_err is None else expert_err
+    check(lib().sx_moe_verify_layer(_p(x), M, _p(Wr), wr_act, rows, E, k, int(shared), shared_id, gate_up.view(),
+                                    down.view(), Ew, _p(logits), _p(ids), _p(coef), _p(h), _p(h_sums), _p(y),
+                                    act_of(x), _p(router_err), _p(expert_err), _p(sync), _s(stream)))
+    return logits, ids, coef, h, y, router_err, expert_err
+
+
 def group_routes(ids, E, ws=None, err=None, stream=None):
     M, A = ids.shape
     nb = route_workspace_bytes(M, A, E)
