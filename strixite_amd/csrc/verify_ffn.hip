@@ -945,7 +945,8 @@ int check_gate_up(const char *fn, int64_t M, int64_t A, int64_t E, int64_t k, in
     SX_CHECK(act == SX_ACT_BF16, fn, " activations must be BF16 (got ", act, ")");
     SX_CHECK(M >= 1 && M <= vf::kMaxTokens && M * A <= vf::kMaxSlots, fn, " M = ", M, ", A = ", A, ": needs M <= ",
              vf::kMaxTokens, " and M * A <= ", vf::kMaxSlots);
-    SX_CHECK(E >= 1 && k >= 1 && k <= E && Ew >= 1 && Ew <= vf::kMaxExperts, fn, " E = ", E, ", k = ", k, ", Ew = ", Ew);
+    SX_CHECK(E >= 1 && E <= vf::kMaxExperts && k >= 1 && k <= E && k <= 32 && Ew >= 1 && Ew <= vf::kMaxExperts, fn,
+             " E = ", E, ", k = ", k, ", Ew = ", Ew, ": needs E, Ew <= ", vf::kMaxExperts, " and k <= min(E, 32)");
     SX_CHECK(w->G == 128 && w->N % Ew == 0 && (w->N / Ew) % 2 == 0, fn, " gate_up view N = ", w->N, ", G = ", w->G,
              ": needs G = 128 and N a multiple of 2 Ew");
     const int64_t K = w->K;
@@ -990,6 +991,8 @@ int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t
              fn, " null pointer");
     if (int rc = check_gate_up(fn, M, A, E, k, Ew, w, act)) return rc;
     SX_CHECK(ld >= E && (shared_logit == nullptr || shared_ld >= 1), fn, " ld = ", ld, ", shared_ld = ", shared_ld);
+    SX_CHECK(shared_logit == nullptr || (shared_id >= 0 && shared_id < Ew), fn, " shared_id = ", shared_id,
+             ", expected the shared expert's row block in 0..", Ew - 1);
     SX_CHECK(aligned(x, 16) && aligned(h, 2), fn, " x must be 16-byte aligned");
     const int64_t I = w->N / Ew / 2;
     SX_CHECK(apart(h, M * A * I * 2, x, M * w->K * 2), fn, " h overlaps x");
@@ -1063,6 +1066,8 @@ int sx_moe_verify_layer(const void *x, int64_t M, const void *wr, int wr_act, in
     SX_CHECK(down->K == I && d == K, fn, " down [", d, ", ", down->K, "] does not match gate_up's I = ", I,
              " and d = ", K);
     SX_CHECK(wr_act == SX_ACT_F32 || wr_act == SX_ACT_BF16, fn, " router weight dtype ", wr_act);
+    SX_CHECK(!shared || (shared_id >= 0 && shared_id < Ew), fn, " shared_id = ", shared_id,
+             ", expected the shared expert's row block in 0..", Ew - 1);
     SX_CHECK(rows >= E + (shared ? 1 : 0) && rows <= vf::kMaxRouterRows, fn, " router weight has ", rows, " rows for E = ", E,
              shared ? " plus the shared gate" : "");
     SX_CHECK(aligned(wr, 16) && aligned(x, 16) && aligned(h, 16) && aligned(h_sums, 16) && aligned(sync, 16), fn,

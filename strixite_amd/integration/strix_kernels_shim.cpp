@@ -1,12 +1,14 @@
 // The reference's operator signatures (strixite kernels/*.hpp, unchanged) on top of libstrixite_amd's C ABI.
 //
-// A maintainer adds this file to strixite's strix_kernels target in place of kernels/linear_q4.hip, linear_q8.hip,
-// moe_router.hip, moe_grouped.hip, swiglu.hip, logits_topk.hip and mtp_pick.hip, and links libstrixite_amd.so; it is
+// A maintainer adds this file to strixite's strix_kernels target in place of kernels/linear.hip, linear_q4.hip,
+// linear_q56.hip, linear_q8.hip, linear_wmma.hip, moe_router.hip, moe_grouped.hip, swiglu.hip, logits_topk.hip and
+// mtp_pick.hip, and links libstrixite_amd.so; it is
 // compiled inside the strixite tree (it includes strixite's own headers), so runtime/qwen4exp.cpp and serve/engine.cpp
 // call the gfx950 kernels without a change. Every function forwards to the sx_* entry point that replaces it and turns
 // a nonzero status into strix::Error with the library's message (common/check.hpp's exception type).
 #include "common/check.hpp"
 #include "common/hip_check.hpp"
+#include "kernels/linear.hpp"
 #include "kernels/linear_q4.hpp"
 #include "kernels/linear_q5.hpp"
 #include "kernels/linear_q6.hpp"
@@ -109,6 +111,16 @@ void linear_q8(const void *x, const Q8DeviceView &w, void *y, int64_t M, Act act
     ok(sx_linear_q8(x, &v, y, M, (int)act, (int)out_act, st(stream)), "linear_q8");
 }
 
+// ---- kernels/linear.hpp: BF16 weights (the router projection, W [E + 1, d]) ----
+void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, Act act,
+                  hipStream_t stream) {
+    linear_bf16w(x, w, y, M, N, K, act, act, stream);
+}
+void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, Act act, Act out_act,
+                  hipStream_t stream) {
+    ok(sx_linear_bf16w(x, w, y, M, N, K, (int)act, (int)out_act, st(stream)), "linear_bf16w");
+}
+
 // ---- kernels/linear_wmma.hpp: the prefill-width dense linears run the same MFMA kernels (16 rows a weight pass) ----
 void linear_q4_wmma(const void *x, const Q4DeviceView &w, void *y, int64_t M, Act act, Act out_act,
                     hipStream_t stream) {
@@ -117,6 +129,10 @@ void linear_q4_wmma(const void *x, const Q4DeviceView &w, void *y, int64_t M, Ac
 void linear_q8_wmma(const void *x, const Q8DeviceView &w, void *y, int64_t M, Act act, Act out_act,
                     hipStream_t stream) {
     linear_q8(x, w, y, M, act, out_act, stream);
+}
+void linear_bf16w_wmma(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, Act act,
+                       Act out_act, hipStream_t stream) {
+    ok(sx_linear_bf16w_wmma(x, w, y, M, N, K, (int)act, (int)out_act, st(stream)), "linear_bf16w_wmma");
 }
 void linear_q5_wmma(const void *, const Q5DeviceView &, void *, int64_t, Act, Act, hipStream_t) {
     STRIX_FAIL("linear_q5_wmma: Q5 weights are not supported on gfx950");

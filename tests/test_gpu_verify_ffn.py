@@ -142,3 +142,12 @@ def test_verify_supported_limits():
     assert kx().verify_supported(16, 4, 8, 4, 8, gu, dn) is True
     assert kx().verify_supported(17, 1, 8, 1, 8, gu, dn) is False  # M > 16
     assert kx().verify_supported(9, 8, 8, 8, 8, gu, dn) is False   # M * A > 64
+    assert kx().verify_supported(1, 4, 1100, 4, 8, gu, dn) is False  # E > 1024 logits: those past 1024 go unread
+    assert kx().verify_supported(1, 32, 40, 32, 8, gu, dn) is True
+    assert kx().verify_supported(1, 33, 40, 33, 8, gu, dn) is False  # k > 32
+    import strixite_amd as sx
+    import torch
+    x = torch.zeros((2, 4096), dtype=torch.bfloat16, device="cuda")
+    logits = torch.zeros((2, 9), dtype=torch.float32, device="cuda")
+    with pytest.raises(sx.SxError, match="shared_id"):  # a shared slot needs a valid expert row block
+        kx().verify_gate_up(x, logits, gu, 8, 4, shared_logit=logits[:, 8:], shared_id=-1)
