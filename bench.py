@@ -360,6 +360,7 @@ def extra_configs(out):
     # config 4: the MoE layer at prefill width, M = 2048, Zipf-skewed routing; grouped MFMA experts
     res["cfg4_prefill_layer"] = prefill_layer()
     res["cfg5_verify_tail"] = verify_tail()
+    res["mtp_draft_head"] = draft_head()
     out["configs"] = res
 
 
@@ -383,6 +384,29 @@ def verify_tail():
     return {"us": round(ms * 1e3, 3), "lm_head_us": round(ms_head * 1e3, 3),
             "lm_head_GBps": round((w.nbytes() + 6 * V * 4) / (ms_head * 1e-3) / 1e9, 1),
             "GBps": round(nb / (ms * 1e-3) / 1e9, 1)}
+
+
+def draft_head():
+    """The MTP draft tail at the served shape: the Q4 copy (G = 64) of the first 65,536 rows of a q8 LM head (d = 4096),
+    made once on the device, then per draft step h [1, 4096] -> logits [1, 65536] -> top-2 pick."""
+    import torch
+
+    from strixite_amd import kernels as kx
+    from strixite_amd import synthetic as syn
+    from strixite_amd.draft import DraftHead
+
+    V, d, mv = 151936, 4096, 65536
+    head = syn.qweight(8, V, d, 64, seed=52)
+    dh = DraftHead(head, mv)
+    # the copy alone (the load-time step; the reference runs it on the host), into the caching allocator's blocks
+    copy_ms = time_window(lambda i: kx.quantize_q4_from_q8(head, 64, rows=mv), min_launches=5, min_ms=20.0, warm_ms=5.0,
+                          windows=3)
+    hs = [syn.activations(1, d, seed=53 + i) for i in range(4)]
+    ms = time_window(lambda i: dh.forward(hs[i % 4]), min_launches=200, windows=3)
+    nb = dh.w.nbytes() + d * 2 + mv * 4 * 2 + 64
+    return {"us": round(ms * 1e3, 3), "GBps": round(nb / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "q4_copy_ms": round(copy_ms, 3),
+            "q4_copy_GBps": round((head.q.numel() // V * mv * 1.5 + mv * (d // 64) * 8) / (copy_ms * 1e-3) / 1e9, 1)}
 
 
 def probe():

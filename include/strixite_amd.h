@@ -190,6 +190,15 @@ int sx_logits_topk_noalloc(const float *logits, int64_t rows, int64_t ld, int64_
                            sx_logit_cand *out, uint32_t *nan, const uint32_t *mask, int64_t mask_words,
                            sx_stream stream);
 
+/* ---- the MTP draft head's Q4 copy of the Q8 LM head: formats/q4_from_q8.hpp:17-27 (quantize_q4_from_q8), which
+ * runtime/qwen4exp.cpp:192-238 runs on the host at load; here on the device, from the resident Q8 rows ----
+ * src: a Q8 view [N, K] (its first N rows: a row prefix of the head); G: the Q4 group (32, 64, 128; the served draft
+ * head uses 64); q [N, K/2], scale / minv [N, K/G] BF16: the Q4 weight, byte-identical to the reference's. A
+ * non-finite dequantized value (the reference throws) sets err {1, row, first k of its group} and that group's scale,
+ * min and codes to zero. */
+int sx_quantize_q4_from_q8(const sx_qview *src, int64_t G, uint8_t *q, uint16_t *scale, uint16_t *minv,
+                           uint32_t *err, sx_stream stream);
+
 /* ---- MTP draft pick, kernels/mtp_pick.hpp:20-33: top-2 + NaN flag + the forward's error words, one 64-byte block.
  * emb_err points at the 8-byte EmbeddingError slot (kernels/embedding.hpp:26-28). ---- */
 typedef struct sx_mtp_pick_s {

@@ -130,6 +130,43 @@ void or_dequant(int bits, const uint8_t *q, const uint16_t *scale, const uint16_
     for (int64_t n = 0; n < N; ++n) dequant_row(bits, q, scale, minv, K, G, n, out + n * K);
 }
 
+int or_quantize_q4(const float *w, int64_t N, int64_t K, int64_t G, uint8_t *q, uint16_t *scale, uint16_t *minv) {
+    const int64_t groups = K / G;
+    std::memset(q, 0, (size_t)(N * K / 2));
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t g = 0; g < groups; ++g) {
+            const float *grp = w + n * K + g * G;
+            float lo = grp[0], hi = grp[0];
+            for (int64_t i = 0; i < G; ++i) {
+                if (!std::isfinite(grp[i])) return 1;
+                lo = std::fmin(lo, grp[i]);
+                hi = std::fmax(hi, grp[i]);
+            }
+            const uint16_t sb = to_bf16((hi - lo) / 15.0f), mb = to_bf16(lo);
+            const float s = bf16f(sb), m = bf16f(mb);
+            scale[n * groups + g] = sb, minv[n * groups + g] = mb;
+            for (int64_t i = 0; i < G; ++i) {
+                int code = 0;
+                if (s > 0.0f) code = (int)std::fmin(std::fmax(std::nearbyint((grp[i] - m) / s), 0.0f), 15.0f);
+                const int64_t k = g * G + i;
+                q[(n * K + k) / 2] |= (uint8_t)(code << ((k & 1) ? 4 : 0));
+            }
+        }
+    return 0;
+}
+
+int or_q4_from_q8(const uint8_t *q8, const uint16_t *s8, const uint16_t *m8, int64_t N, int64_t K, int64_t G8,
+                  int64_t G4, uint8_t *q4, uint16_t *s4, uint16_t *m4, int threads) {
+    std::atomic<int> bad{0};
+    parallel_for(N, threads, [&](int64_t n) {
+        std::vector<float> w((size_t)K);
+        dequant_row(8, q8, s8, m8, K, G8, n, w.data());
+        // row n of the result: its own slice of each output array (groups run along K inside a row)
+        if (or_quantize_q4(w.data(), 1, K, G4, q4 + n * K / 2, s4 + n * (K / G4), m4 + n * (K / G4))) bad = 1;
+    });
+    return bad.load();
+}
+
 void or_linear_q(int bits, const void *x, const uint8_t *q, const uint16_t *scale, const uint16_t *minv, int64_t N,
                  int64_t K, int64_t G, void *y, int64_t M, int act, int out_act, int threads) {
     std::vector<std::vector<double>> xs;

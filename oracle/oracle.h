@@ -25,6 +25,15 @@ uint16_t or_f32_to_bf16(float f);
 void or_dequant(int bits, const uint8_t *q, const uint16_t *scale, const uint16_t *minv, int64_t N, int64_t K,
                 int64_t G, float *out);
 
+/* formats/q4.cpp:44-86 quantize_q4 on finite FP32 w [N, K]: per group lo/hi, s = bf16((hi - lo) / 15),
+ * m = bf16(lo), code = clamp(nearbyint((w - m) / s), 0, 15) (0 when s = 0). Returns 0, or 1 on a non-finite weight. */
+int or_quantize_q4(const float *w, int64_t N, int64_t K, int64_t G, uint8_t *q, uint16_t *scale, uint16_t *minv);
+
+/* formats/q4_from_q8.cpp:34-86: a Q8 weight's rows dequantized exactly (q8.cpp:117-127), then quantize_q4 with group
+ * G4. Returns 0, or 1 on a non-finite dequantized value. */
+int or_q4_from_q8(const uint8_t *q8, const uint16_t *s8, const uint16_t *m8, int64_t N, int64_t K, int64_t G8,
+                  int64_t G4, uint8_t *q4, uint16_t *s4, uint16_t *m4, int threads);
+
 /* kernels/linear_q4.hpp:26-30, linear_q8.hpp:13-14: y[M,N] = x[M,K] * deq(W)^T, x in act, y in out_act.
  * threads <= 0: all hardware threads. */
 void or_linear_q(int bits, const void *x, const uint8_t *q, const uint16_t *scale, const uint16_t *minv, int64_t N,

@@ -43,6 +43,10 @@ def lib():
         L.or_dequant.argtypes = [_INT, _P, _P, _P, _I64, _I64, _I64, _P]
         L.or_linear_q.argtypes = [_INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _INT, _INT, _INT]
         L.or_linear_f32w.argtypes = [_P, _P, _I64, _I64, _P, _I64, _INT, _INT]
+        L.or_quantize_q4.argtypes = [_P, _I64, _I64, _I64, _P, _P, _P]
+        L.or_quantize_q4.restype = _INT
+        L.or_q4_from_q8.argtypes = [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _INT]
+        L.or_q4_from_q8.restype = _INT
         L.or_linear_bf16w.argtypes = [_P, _P, _I64, _I64, _P, _I64, _INT, _INT, _INT]
         L.or_moe_shared_add.argtypes = [_P, _P, _P, _I64, _I64, _I64, ctypes.c_uint32, _P, _P, _I64, _INT, _P]
         L.or_moe_router.argtypes = [_P, _I64, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _P]
@@ -116,6 +120,29 @@ def linear_f32w(x, W, threads=0):
     lib().or_linear_f32w(_ptr(np.ascontiguousarray(x)), _ptr(np.ascontiguousarray(W, np.float32)), N, K, _ptr(y), M,
                          act, threads)
     return y
+
+
+def quantize_q4(w, G):
+    """formats/q4.cpp quantize_q4 restated: FP32 [N, K] -> QWeight (q4)."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    q = np.empty(N * K // 2, np.uint8)
+    s = np.empty(N * (K // G), np.uint16)
+    m = np.empty(N * (K // G), np.uint16)
+    if lib().or_quantize_q4(_ptr(w), N, K, G, _ptr(q), _ptr(s), _ptr(m)):
+        raise ValueError("quantize_q4: non-finite weight")
+    return QWeight(4, q, s, m, N, K, G)
+
+
+def q4_from_q8(w8, G4, threads=0):
+    """formats/q4_from_q8.cpp restated: a q8 QWeight -> the q4 QWeight of its exactly dequantized rows."""
+    N, K = w8.N, w8.K
+    q = np.empty(N * K // 2, np.uint8)
+    s = np.empty(N * (K // G4), np.uint16)
+    m = np.empty(N * (K // G4), np.uint16)
+    if lib().or_q4_from_q8(*w8.args(), N, K, w8.G, G4, _ptr(q), _ptr(s), _ptr(m), threads):
+        raise ValueError("q4_from_q8: non-finite dequantized weight")
+    return QWeight(4, q, s, m, N, K, G4)
 
 
 def linear_bf16w(x, W, out_act=None, threads=0):
@@ -256,6 +283,8 @@ def ref():
         L.ref_quantize.restype = _INT
         L.ref_dequantize.argtypes = [_INT, _P, _P, _P, _I64, _I64, _I64, _P]
         L.ref_dequantize.restype = _INT
+        L.ref_q4_from_q8.argtypes = [_P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P, _P, _P]
+        L.ref_q4_from_q8.restype = _INT
         L.ref_top2.argtypes = [_P, _I64, _P, _P, _P, _P]
         L.ref_sampler_new.argtypes = [_D, _I64, _D, ctypes.c_uint64, _I64]
         L.ref_sampler_new.restype = _P
@@ -279,6 +308,16 @@ def ref_quantize(bits, w, G):
     if rc != 0:
         raise ValueError("reference quantize refused the input")
     return QWeight(bits, q, s, m, N, K, G), d
+
+
+def ref_q4_from_q8(w8, G4, threads=4):
+    N, K = w8.N, w8.K
+    q = np.empty(N * K // 2, np.uint8)
+    s = np.empty(N * (K // G4), np.uint16)
+    m = np.empty(N * (K // G4), np.uint16)
+    if ref().ref_q4_from_q8(*w8.args(), N, K, w8.G, G4, threads, _ptr(q), _ptr(s), _ptr(m)) != 0:
+        raise ValueError("reference quantize_q4_from_q8 refused the input")
+    return QWeight(4, q, s, m, N, K, G4)
 
 
 def ref_dequantize(w):

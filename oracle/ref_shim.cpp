@@ -1,7 +1,8 @@
-// extern "C" entry points over the reference's own host code (formats/q4.cpp, formats/q8.cpp, serve/sampler.cpp),
+// extern "C" entry points over the reference's own host code (formats/q4.cpp, q8.cpp, q4_from_q8.cpp, serve/sampler.cpp),
 // compiled from /root/reference by oracle/Makefile into oracle/_ref/libstrix_ref.so. Test infrastructure only: it is
 // the reference itself, used to pin the oracle restatement and to write the fixtures under tests/golden/.
 #include "formats/q4.hpp"
+#include "formats/q4_from_q8.hpp"
 #include "formats/q8.hpp"
 #include "serve/sampler.hpp"
 
@@ -29,6 +30,25 @@ int ref_quantize(int bits, const float *w, int64_t N, int64_t K, int64_t G, uint
             const std::vector<float> d = strix::dequantize_q8(r);
             std::memcpy(deq, d.data(), 4 * d.size());
         }
+        return 0;
+    } catch (const std::exception &) {
+        return 1;
+    }
+}
+
+// formats/q4_from_q8.hpp:23 quantize_q4_from_q8 on a caller-supplied Q8 weight; the Q4 result's arrays into q4, s4,
+// m4. Returns 0, or 1 if the reference threw.
+int ref_q4_from_q8(const uint8_t *q, const uint16_t *scale, const uint16_t *minv, int64_t N, int64_t K, int64_t G8,
+                   int64_t G4, int threads, uint8_t *q4, uint16_t *s4, uint16_t *m4) {
+    try {
+        strix::Q8Weight w;
+        w.N = N, w.K = K, w.G = G8;
+        const size_t groups = (size_t)(N * (K / G8));
+        w.q.assign(q, q + N * K), w.scale.assign(scale, scale + groups), w.minv.assign(minv, minv + groups);
+        const strix::Q4Weight r = strix::quantize_q4_from_q8(w, G4, threads);
+        std::memcpy(q4, r.q.data(), r.q.size());
+        std::memcpy(s4, r.scale.data(), 2 * r.scale.size());
+        std::memcpy(m4, r.minv.data(), 2 * r.minv.size());
         return 0;
     } catch (const std::exception &) {
         return 1;

@@ -79,6 +79,7 @@ SIGNATURES = {
     "sx_logits_topk_workspace_bytes": [_I64, _I64, _I64, _SZP],
     "sx_logits_topk": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, ctypes.c_size_t, _P, _I64, _P],
     "sx_logits_topk_noalloc": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P],
+    "sx_quantize_q4_from_q8": [_QV, _I64, _P, _P, _P, _P, _P],
     "sx_mtp_pick": [_P, _I64, _P, _P, _P, _P, _P, _P],
     "sx_mtp_accept": [_P, _P, _I64, _P, _I64, _P, _D, _I64, _D, _I64, _P, _P],
 }

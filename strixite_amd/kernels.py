@@ -301,6 +301,19 @@ def logits_topk_noalloc(logits, n_valid, k=20, mask=None, out=None, nan=None, st
     return out[..., 0].view(torch.float32), out[..., 1], nan, out
 
 
+def quantize_q4_from_q8(w8, G=64, rows=None, err=None, stream=None):
+    """The Q4 copy of the first `rows` rows of a Q8 weight (formats/q4_from_q8.hpp), made on the device: a QWeight."""
+    rows = w8.N if rows is None else rows
+    dev = w8.q.device
+    q = torch.empty(rows * w8.K // 2, dtype=torch.uint8, device=dev)
+    s = torch.empty(rows * (w8.K // G), dtype=torch.int16, device=dev)
+    m = torch.empty(rows * (w8.K // G), dtype=torch.int16, device=dev)
+    err = _err(dev) if err is None else err
+    src = QView(w8.q.data_ptr(), w8.scale.data_ptr(), w8.minv.data_ptr(), rows, w8.K, w8.G)
+    check(lib().sx_quantize_q4_from_q8(ctypes.byref(src), G, _p(q), _p(s), _p(m), _p(err), _s(stream)))
+    return QWeight(4, q, s, m, rows, w8.K, G), err
+
+
 def mtp_pick(logits, router_err, expert_err, attn_err, emb_err, out=None, stream=None):
     out = torch.empty(64, dtype=torch.uint8, device=logits.device) if out is None else out
     check(lib().sx_mtp_pick(_p(logits), logits.numel(), _p(router_err), _p(expert_err), _p(attn_err), _p(emb_err),

@@ -8,6 +8,9 @@ Each fixture holds seeded inputs and the reference's outputs, nothing else:
   sampler.npz  Sampler::sample (serve/sampler.cpp:103-328), one call per row in sequence, for several parameter sets
   accept.npz   the engine's accept loop (serve/engine.cpp:592-610) driven by the reference Sampler, drafts built so
                the accepted length is each of 0..5, greedy and sampled (T 0.7, top-k 40, top-p 0.95)
+  q4_from_q8.npz  formats/q4_from_q8.cpp quantize_q4_from_q8 (the MTP draft head's Q4 copy) of seeded Q8 weights:
+               Q8 groups 64 and 128 into Q4 groups 32, 64, 128, with constant, one-code and wide groups
+Run with fixture names (e.g. `make_golden.py q4_from_q8`) to write only those.
 """
 import os
 import sys
@@ -138,13 +141,34 @@ def accept():
                         j=np.array([c[6] for c in cases], np.int64), tokens=np.stack([c[7] for c in cases]))
 
 
+def q4_from_q8():
+    rng = np.random.default_rng(5)
+    out = {}
+    for G8, G4 in ((64, 64), (64, 128), (64, 32), (128, 64)):
+        N, K = 24, 512
+        q = rng.integers(0, 256, N * K, dtype=np.uint8)
+        s = (np.abs(rng.standard_normal(N * (K // G8))) * 0.02).astype(np.float32)
+        sb = (s.view(np.uint32) >> 16).astype(np.uint16)  # truncated to BF16: any BF16 scale will do
+        mb = ((-127.5 * (sb.astype(np.uint32) << 16).view(np.float32)).view(np.uint32) >> 16).astype(np.uint16)
+        q.reshape(N, K)[1, :G8] = 77                       # one code in a group: a constant Q4 group (s = 0)
+        q.reshape(N, K)[2, :] = rng.integers(0, 2, K)      # two codes only
+        sb.reshape(N, K // G8)[3, 0] = 0                   # zero scale: constant dequantized values
+        sb.reshape(N, K // G8)[4, 0] = 0x4100              # a wide group (scale 8.0)
+        w8 = orc.QWeight(8, q, sb, mb, N, K, G8)
+        r = orc.ref_q4_from_q8(w8, G4)
+        tag = f"g{G8}_g{G4}"
+        out[tag + "_q8"], out[tag + "_s8"], out[tag + "_m8"] = q, sb, mb
+        out[tag + "_q4"], out[tag + "_s4"], out[tag + "_m4"] = r.q, r.scale, r.minv
+    out["shape"] = np.array([24, 512], np.int64)
+    np.savez_compressed(os.path.join(HERE, "q4_from_q8.npz"), **out)
+
+
 if __name__ == "__main__":
     if not orc.ref_available():
         orc.build()
-    formats()
-    top2()
-    sampler()
-    accept()
+    todo = sys.argv[1:] or ["formats", "top2", "sampler", "accept", "q4_from_q8"]
+    for name in todo:
+        globals()[name]()
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

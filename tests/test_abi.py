@@ -90,3 +90,20 @@ def test_topk_workspace_and_reports(L):
     assert b"expert id 700 at slot 5" in L.sx_last_error()
     e = (ctypes.c_uint32 * 3)(0, 0, 0)
     assert L.sx_report_router_error(e, b"x") == sx.SX_OK
+
+
+def test_engine_draft_and_commit_rules():
+    """serve/engine.cpp:574-581 (a draft is kept when its top-1 margin reaches mtp_margin and it is no end token; NaN is
+    an error) and :612-645 (keep every verify row when all drafts were accepted, else the verified token and the
+    accepted drafts)."""
+    from strixite_amd import MtpPick
+    from strixite_amd.draft import commit_after_accept, draft_continues
+    p = MtpPick(best=5, best_v=3.0, second_v=1.0, nan=0)
+    assert draft_continues(p, 2.0, {7, 8}) and not draft_continues(p, 2.5, {7, 8})
+    assert not draft_continues(MtpPick(best=7, best_v=9.0, second_v=1.0, nan=0), 2.0, {7, 8})
+    with pytest.raises(RuntimeError):
+        draft_continues(MtpPick(best=0, best_v=0.0, second_v=0.0, nan=1), 2.0, set())
+    assert commit_after_accept(5, 5) == ("keep_verify", 6)
+    assert [commit_after_accept(j, 5) for j in range(5)] == [("keep_verify_prefix", j + 1) for j in range(5)]
+    with pytest.raises(ValueError):
+        commit_after_accept(6, 5)

@@ -49,6 +49,36 @@ def test_dequant_nibble_order():
     assert d[0, 0] == 1.0 and d[0, 1] == 2.0 and np.all(d[0, 2:] == 0)
 
 
+@pytest.mark.parametrize("G", [32, 64, 128])
+def test_quantize_q4_matches_reference_fixture(golden_dir, G):
+    """quantize_q4 restated (formats/q4.cpp:44-86) against the compiled reference's codes, scales and mins on the
+    formats fixture's weights (constant, negative-constant and wide groups included)."""
+    f = np.load(os.path.join(golden_dir, "formats.npz"))
+    tag = f"q4_g{G}"
+    w = orc.quantize_q4(f[tag + "_w"], G)
+    assert np.array_equal(w.q, f[tag + "_q"]) and np.array_equal(w.scale, f[tag + "_scale"])
+    assert np.array_equal(w.minv, f[tag + "_min"])
+
+
+@pytest.mark.parametrize("tag", ["g64_g64", "g64_g128", "g64_g32", "g128_g64"])
+def test_q4_from_q8_matches_reference_fixture(golden_dir, tag):
+    """The draft head's Q4 copy (formats/q4_from_q8.cpp) restated: byte-identical to the compiled reference's."""
+    f = np.load(os.path.join(golden_dir, "q4_from_q8.npz"))
+    N, K = (int(v) for v in f["shape"])
+    G8, G4 = (int(t[1:]) for t in tag.split("_"))
+    w8 = orc.QWeight(8, f[tag + "_q8"], f[tag + "_s8"], f[tag + "_m8"], N, K, G8)
+    w4 = orc.q4_from_q8(w8, G4)
+    assert np.array_equal(w4.q, f[tag + "_q4"]) and np.array_equal(w4.scale, f[tag + "_s4"])
+    assert np.array_equal(w4.minv, f[tag + "_m4"])
+
+
+@pytest.mark.skipif(not orc.ref_available(), reason="oracle/_ref not built (needs the reference tree)")
+def test_q4_from_q8_matches_live_reference():
+    w8 = util.rand_qweight(np.random.default_rng(6), 8, 300, 1024, 64)
+    a, b = orc.q4_from_q8(w8, 64), orc.ref_q4_from_q8(w8, 64)
+    assert np.array_equal(a.q, b.q) and np.array_equal(a.scale, b.scale) and np.array_equal(a.minv, b.minv)
+
+
 # ---------------- dense linear (a3 / a4) ----------------
 
 @pytest.mark.parametrize("bits", [4, 8])
