@@ -223,6 +223,78 @@ int sx_mtp_accept(const sx_logit_cand *cands, const uint32_t *nan, int64_t kc, c
                   const double *u, double temperature, int64_t top_k, double top_p, int64_t n_valid, int32_t *out,
                   sx_stream stream);
 
+/* ---- strixw weight files: formats/strixw.hpp (the reader, StrixwFile :86-112) and runtime/strixw_loader.hpp (the
+ * upload, StrixwDevice :22-52) ----
+ * A file is a 128-byte header (magic "STRIXWT\0", format version 1..4, index and data-region offsets, file size, the
+ * index's and the header's own strix_hash64), an index (metadata key/value pairs; one record per tensor: name,
+ * encoding, shape, group size, experts, source parts, and each component's role, absolute offset, size and hash) and
+ * a data region on a 4096-byte boundary: tensors start on 4096-byte boundaries, components on 256-byte ones.
+ * Encodings and component roles carry the file's own numbering (formats/strixw.hpp:17-19). */
+enum sx_strixw_encoding {
+    SX_STRIXW_Q4 = 1, SX_STRIXW_Q4_CHUNK_MAJOR = 2, SX_STRIXW_BF16 = 3, SX_STRIXW_F32 = 4, SX_STRIXW_I64 = 5,
+    SX_STRIXW_Q8 = 6, SX_STRIXW_Q8_CHUNK_MAJOR = 7, SX_STRIXW_Q6 = 8, SX_STRIXW_Q5 = 9
+};
+enum sx_strixw_role { SX_STRIXW_DATA = 0, SX_STRIXW_Q = 1, SX_STRIXW_SCALE = 2, SX_STRIXW_MIN = 3 };
+
+typedef struct sx_strixw sx_strixw; /* an open, validated file (read-only mapping) */
+
+/* StrixwComponent (formats/strixw.hpp:30-33): offset absolute in the file. */
+typedef struct sx_strixw_component {
+    uint8_t role;
+    uint64_t offset, bytes, hash;
+} sx_strixw_component;
+
+/* StrixwTensor (formats/strixw.hpp:35-44); name points into the open file and lives as long as it. */
+typedef struct sx_strixw_tensor {
+    const char *name;
+    int32_t encoding, ndim;
+    int64_t shape[8];
+    int64_t group_size, experts;
+    int32_t nparts, ncomp;
+    sx_strixw_component comp[4];
+} sx_strixw_tensor;
+
+/* strix_hash64 (formats/strixw.hpp:50): the file's 64-bit checksum of n bytes (host memory). */
+uint64_t sx_strix_hash64(const void *data, uint64_t n);
+/* StrixwFile::StrixwFile (formats/strixw.hpp:88): maps path and validates the header, the index and every record
+ * (the same checks, in the same order, as formats/strixw.cpp:398-500); on failure SX_EINVAL with a message naming the
+ * file and the problem ("bad magic", "header hash mismatch", "truncated", "components overlap", ...), *out NULL.
+ * Host only: no HIP call. */
+int sx_strixw_open(const char *path, sx_strixw **out);
+void sx_strixw_close(sx_strixw *f);
+/* version, file_bytes, data_offset, tensor and metadata counts (any pointer may be NULL). */
+int sx_strixw_summary(const sx_strixw *f, uint32_t *version, uint64_t *file_bytes, uint64_t *data_offset,
+                      int64_t *tensors, int64_t *meta);
+/* StrixwFile::meta() (formats/strixw.hpp:95-96): the i-th pair in the file's key order, or the value of `key`
+ * (SX_EINVAL naming the file when absent). Strings live as long as the file. */
+int sx_strixw_meta_at(const sx_strixw *f, int64_t i, const char **key, const char **value);
+int sx_strixw_meta(const sx_strixw *f, const char *key, const char **value);
+/* StrixwFile::find / tensors() (formats/strixw.hpp:97-98): *index = the record's position, or -1 when absent. */
+int sx_strixw_find(const sx_strixw *f, const char *name, int64_t *index);
+int sx_strixw_tensor_at(const sx_strixw *f, int64_t i, sx_strixw_tensor *out);
+/* StrixwPart (formats/strixw.hpp:25-28) of a record: the checkpoint tensor and the rows it fills. */
+int sx_strixw_part_at(const sx_strixw *f, int64_t tensor, int64_t part, const char **source, int64_t *row_offset,
+                      int64_t *rows);
+/* StrixwFile::verify_hashes (formats/strixw.hpp:102): rehashes every component on `threads` host threads; SX_EINVAL
+ * naming the first corrupt component in file order. */
+int sx_strixw_verify_hashes(const sx_strixw *f, int threads);
+/* StrixwDevice::StrixwDevice (runtime/strixw_loader.hpp:27): copies the data region (file_bytes - data_offset bytes)
+ * to dst (device memory of at least that size, 256-byte aligned, owned by the caller) through pinned staging slots
+ * filled by read_threads (1..64) concurrent pread()s, the copies queued on `stream`. Synchronous: returns once the
+ * region is on the device; *seconds (may be NULL) = wall time. Component hashes are not rechecked (the header and
+ * index hashes were, at open). */
+int sx_strixw_load(const sx_strixw *f, void *dst, uint64_t dst_bytes, int read_threads, double *seconds,
+                   sx_stream stream);
+/* StrixwDevice::q4 / q8 / qw (runtime/strixw_loader.hpp:36-41): the view of a row-major q4 (bits 4), q8 (8) or either
+ * (0) tensor of shape [N, K], checked, with pointers into the region loaded at `base` (base + offset - data_offset),
+ * or into the file's mapping when base is NULL. */
+int sx_strixw_qview(const sx_strixw *f, const void *base, const char *name, int bits, int64_t N, int64_t K,
+                    sx_qview *out);
+/* StrixwDevice::bf16 / f32 (runtime/strixw_loader.hpp:46-47), and i64: a dense tensor's data, encoding and shape
+ * checked; base as for sx_strixw_qview. */
+int sx_strixw_data(const sx_strixw *f, const void *base, const char *name, int encoding, const int64_t *shape,
+                   int ndim, const void **out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -491,3 +491,29 @@ int64_t or_accept(or_rng *r, const float *logits, int64_t k, int64_t row_len, in
 }
 
 }  // extern "C"
+
+uint64_t or_strix_hash64(const uint8_t *p, uint64_t n) {
+    const uint64_t A = 0x9e3779b97f4a7c15ull, B = 0xd6e8feb86659fd93ull;
+    auto absorb = [&](uint64_t h, uint64_t w) {
+        const uint64_t x = h ^ (w * A);
+        return (x ^ (x >> 31)) * B;
+    };
+    uint64_t lanes[4] = {n ^ A, n ^ B, ~n ^ A, ~n ^ B};
+    const uint64_t words = n / 8;
+    for (uint64_t i = 0; i < words; ++i) {
+        uint64_t w = 0;
+        for (int b = 7; b >= 0; --b) w = (w << 8) | p[8 * i + b];
+        lanes[i % 4] = absorb(lanes[i % 4], w);
+    }
+    const uint64_t rest = n - 8 * words;
+    if (rest) {
+        uint64_t w = rest << 56;
+        for (uint64_t b = 0; b < rest; ++b) w ^= (uint64_t)p[8 * words + b] << (8 * b);
+        lanes[0] = absorb(lanes[0], w);
+    }
+    uint64_t r = lanes[0];
+    for (int l = 1; l < 4; ++l) r = absorb(r, lanes[l]);
+    r ^= r >> 33;
+    r *= A;
+    return r ^ (r >> 29);
+}

@@ -103,6 +103,13 @@ int32_t or_sample_row(or_rng *r, const float *logits, int64_t n_valid, double te
 int64_t or_accept(or_rng *r, const float *logits, int64_t k, int64_t row_len, int64_t n_valid, const int32_t *drafts,
                   double temperature, int64_t top_k, double top_p, int32_t *sampled, int32_t *status);
 
+// strix_hash64 (formats/strixw.cpp:253-274), restated word by word: the n / 8 whole little-endian 8-byte words go, in
+// order, to lane (word index mod 4) - the reference's 32-byte blocks and then its leftover words land on the same
+// lanes - each absorbed as lane = ((lane ^ w*A) ^ ((lane ^ w*A) >> 31)) * B; the 1..7 trailing bytes, zero-padded,
+// with their count in the top byte, go to lane 0; the lanes start from n and ~n xor A / B and fold 0..3 in order,
+// then r ^= r >> 33, r *= A, r ^= r >> 29.
+uint64_t or_strix_hash64(const uint8_t *p, uint64_t n);
+
 #ifdef __cplusplus
 }
 #endif

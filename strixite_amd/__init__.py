@@ -40,8 +40,23 @@ class MtpPick(ctypes.Structure):
                 ("emb", ctypes.c_ulonglong)]
 
 
+class StrixwComponentC(ctypes.Structure):
+    """sx_strixw_component: StrixwComponent (formats/strixw.hpp:30-33)."""
+    _fields_ = [("role", ctypes.c_uint8), ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64),
+                ("hash", ctypes.c_uint64)]
+
+
+class StrixwTensorC(ctypes.Structure):
+    """sx_strixw_tensor: StrixwTensor (formats/strixw.hpp:35-44)."""
+    _fields_ = [("name", ctypes.c_char_p), ("encoding", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("shape", ctypes.c_int64 * 8), ("group_size", ctypes.c_int64), ("experts", ctypes.c_int64),
+                ("nparts", ctypes.c_int32), ("ncomp", ctypes.c_int32), ("comp", StrixwComponentC * 4)]
+
+
 _P, _I64, _INT, _D, _SZP = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double, ctypes.POINTER(ctypes.c_size_t)
 _QV = ctypes.POINTER(QView)
+_U64, _CP, _PCP = ctypes.c_uint64, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)
+_PI64 = ctypes.POINTER(ctypes.c_int64)
 
 # name -> argtypes (restype int unless listed in _RESTYPES). Every symbol include/strixite_amd.h declares.
 SIGNATURES = {
@@ -82,8 +97,23 @@ SIGNATURES = {
     "sx_quantize_q4_from_q8": [_QV, _I64, _P, _P, _P, _P, _P],
     "sx_mtp_pick": [_P, _I64, _P, _P, _P, _P, _P, _P],
     "sx_mtp_accept": [_P, _P, _I64, _P, _I64, _P, _D, _I64, _D, _I64, _P, _P],
+    "sx_strix_hash64": [_P, _U64],
+    "sx_strixw_open": [_CP, ctypes.POINTER(_P)],
+    "sx_strixw_close": [_P],
+    "sx_strixw_summary": [_P, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_U64), ctypes.POINTER(_U64), _PI64,
+                          _PI64],
+    "sx_strixw_meta_at": [_P, _I64, _PCP, _PCP],
+    "sx_strixw_meta": [_P, _CP, _PCP],
+    "sx_strixw_find": [_P, _CP, _PI64],
+    "sx_strixw_tensor_at": [_P, _I64, ctypes.POINTER(StrixwTensorC)],
+    "sx_strixw_part_at": [_P, _I64, _I64, _PCP, _PI64, _PI64],
+    "sx_strixw_verify_hashes": [_P, _INT],
+    "sx_strixw_load": [_P, _P, _U64, _INT, ctypes.POINTER(_D), _P],
+    "sx_strixw_qview": [_P, _P, _CP, _INT, _I64, _I64, _QV],
+    "sx_strixw_data": [_P, _P, _CP, _INT, _PI64, _INT, ctypes.POINTER(_P)],
 }
-_RESTYPES = {"sx_last_error": ctypes.c_char_p, "sx_version": ctypes.c_char_p}
+_RESTYPES = {"sx_last_error": ctypes.c_char_p, "sx_version": ctypes.c_char_p, "sx_strix_hash64": _U64,
+             "sx_strixw_close": None}
 
 _lib = None
 

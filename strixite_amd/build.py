@@ -46,7 +46,7 @@ def _compile(src):
 
 def build(jobs=None, verbose=True):
     os.makedirs(OUT, exist_ok=True)
-    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
     jobs = jobs or min(len(srcs), max(1, os.cpu_count() or 1), 16)
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, srcs))

@@ -10,6 +10,9 @@ Each fixture holds seeded inputs and the reference's outputs, nothing else:
                the accepted length is each of 0..5, greedy and sampled (T 0.7, top-k 40, top-p 0.95)
   q4_from_q8.npz  formats/q4_from_q8.cpp quantize_q4_from_q8 (the MTP draft head's Q4 copy) of seeded Q8 weights:
                Q8 groups 64 and 128 into Q4 groups 32, 64, 128, with constant, one-code and wide groups
+  strixw_small.strixw  a file written by formats/strixw.cpp's StrixwWriter from oracle/strixw.py's sample_plan()
+               (every encoding, metadata, parts)
+  strixw_hash.npz  strix_hash64 (formats/strixw.cpp:253-274) of seeded buffers of every length 0..300 and some long ones
 Run with fixture names (e.g. `make_golden.py q4_from_q8`) to write only those.
 """
 import os
@@ -163,10 +166,26 @@ def q4_from_q8():
     np.savez_compressed(os.path.join(HERE, "q4_from_q8.npz"), **out)
 
 
+def strixw():
+    from oracle import strixw as sw
+    meta, specs, payloads = sw.sample_plan(seed=7)
+    sw.ref_write(os.path.join(HERE, "strixw_small.strixw"), meta, specs, payloads)
+    rng = np.random.default_rng(8)
+    lens = list(range(301)) + [1023, 4096, 4099, 65536 + 13]
+    data = rng.integers(0, 256, sum(lens), dtype=np.uint8)
+    hashes = np.zeros(len(lens), dtype=np.uint64)
+    at = 0
+    for i, n in enumerate(lens):
+        hashes[i] = sw.ref_hash64(data[at:at + n].tobytes())
+        at += n
+    np.savez_compressed(os.path.join(HERE, "strixw_hash.npz"), data=data, lens=np.array(lens, dtype=np.int64),
+                        hash=hashes)
+
+
 if __name__ == "__main__":
     if not orc.ref_available():
         orc.build()
-    todo = sys.argv[1:] or ["formats", "top2", "sampler", "accept", "q4_from_q8"]
+    todo = sys.argv[1:] or ["formats", "top2", "sampler", "accept", "q4_from_q8", "strixw"]
     for name in todo:
         globals()[name]()
     for f in sorted(os.listdir(HERE)):

@@ -22,7 +22,7 @@ def L():
 
 def declared():
     text = open(HEADER).read()
-    return set(re.findall(r"^\s*(?:int|const char \*)\s*(sx_\w+)\s*\(", text, re.M))
+    return set(re.findall(r"^\s*(?:int|const char \*|uint64_t|void)\s*(sx_\w+)\s*\(", text, re.M))
 
 
 def test_header_and_python_signatures_agree():
@@ -33,7 +33,7 @@ def declared_arity():
     """name -> number of parameters, parsed from the header's prototypes."""
     text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
     out = {}
-    for m in re.finditer(r"^\s*(?:int|const char \*)\s*(sx_\w+)\s*\(([^;]*?)\)\s*;", text, re.M | re.S):
+    for m in re.finditer(r"^\s*(?:int|const char \*|uint64_t|void)\s*(sx_\w+)\s*\(([^;]*?)\)\s*;", text, re.M | re.S):
         args = m.group(2).strip()
         out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
     return out
