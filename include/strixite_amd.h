@@ -127,9 +127,10 @@ int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A,
  * expert_err {1, 0xFFFFFFFE, phase} instead of hanging. */
 int sx_moe_verify_layer_sync_bytes(size_t *bytes);
 /* Diagnostic: a device buffer of (compute units x 16) uint64 that later sx_moe_verify_layer launches (any thread) fill
- * with each block's phase timestamps (s_memrealtime, 100 MHz): [0] start, [1] projection items done, [3] first gate_up
- * weight loads issued (routing done), [4] gate_up done, [5] h complete, [6] h staged,
- * [7] end. NULL turns it off (the default). No reference counterpart: the
+ * with each block's phase timestamps (s_memrealtime, 100 MHz): [0] start, [1] projection items done, [2] logits
+ * fresh (wave 0), [8] tokens routed, [9] expert list built, [3] first gate_up weight loads issued, [4] gate_up done,
+ * [5] h complete, [6] h staged, [7] end; and two counts: [10] polls of the logits, [11] gate_up rounds taken. NULL
+ * turns it off (the default). No reference counterpart: the
  * reference's tracing (common/trace.hpp) marks host-side launch ranges, which cannot show phases inside a launch. */
 int sx_moe_verify_layer_trace(uint64_t *buf);
 int sx_moe_verify_layer(const void *x, int64_t M, const void *wr, int wr_act, int64_t rows, int64_t E, int64_t k,

@@ -144,14 +144,17 @@ __device__ void route_values(float (&v)[NV], int E, int k, bool has_shared, floa
     uint32_t lm = hv[0];
 #pragma unroll
     for (int j = 1; j < NV; ++j) lm = max(lm, hv[j]);
+    // Only the top 16 bits of T are searched (8 steps): a T with its low bits cleared is still <= the k-th largest
+    // lane maximum, so the candidate set still holds the top k; it admits at most a few more (values within a
+    // 2^-7 relative distance of the threshold).
     uint32_t T = 0u;
-    for (int b = 30; b >= 0; b -= 2) {  // two bits a step: three independent counts
+    for (int b = 30; b >= 16; b -= 2) {  // two bits a step: three independent counts
         const uint32_t t1 = T | (1u << b), t2 = T | (2u << b), t3 = T | (3u << b);
         const int c1 = __popcll(__ballot(lm >= t1)), c2 = __popcll(__ballot(lm >= t2)), c3 = __popcll(__ballot(lm >= t3));
         T = c3 >= k ? t3 : c2 >= k ? t2 : c1 >= k ? t1 : T;  // uniform
     }
     // the candidates' keys (value desc, index asc as one unsigned order) into this wave's LDS row, in (j, lane) order
-    __shared__ uint64_t route_cand[16][64];
+    __shared__ __attribute__((aligned(16))) uint64_t route_cand[16][64];
     uint64_t *cand = route_cand[(threadIdx.x >> 6) & 15];
     int C = 0;
 #pragma unroll
@@ -166,11 +169,12 @@ __device__ void route_values(float (&v)[NV], int E, int k, bool has_shared, floa
         // one wave's LDS accesses take effect in program order: the writes above precede these reads
         const uint64_t mine = lane < C ? cand[lane] : 0ull;
         int rank = 0;
-        for (int c = 0; c < C; c += 4) {  // uniform
+        for (int c = 0; c < C; c += 8) {  // uniform; 16-byte broadcast reads, eight keys a step (past C: ignored)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint64_t o = cand[min(c + u, C - 1)];
-                rank += (c + u < C && o > mine) ? 1 : 0;
+            for (int u = 0; u < 8; u += 2) {
+                const ulonglong2 o = *reinterpret_cast<const ulonglong2 *>(cand + c + u);
+                rank += (c + u < C && o.x > mine) ? 1 : 0;
+                rank += (c + u + 1 < C && o.y > mine) ? 1 : 0;
             }
         }
         if (lane >= C) rank = lane;  // ranks 0 .. C-1 of the candidates plus the other lanes: a permutation

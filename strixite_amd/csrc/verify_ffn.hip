@@ -46,8 +46,8 @@ constexpr int kZeroBytes = qmm::detail::kZeroBytes;
 struct Routes {                // one block's copy of the routing (LDS)
     int32_t ids[kMaxSlots];    // slot s = m * A + a
     float coef[kMaxSlots];
-    int32_t u_exp[kMaxSlots];  // distinct valid experts, ascending
-    uint32_t u_mask[kMaxSlots];  // their tokens (bit m)
+    int32_t u_exp[kMaxSlots + 1];  // distinct valid experts, ascending (entry kMaxSlots: a write sink)
+    uint32_t u_mask[kMaxSlots + 1];  // their tokens (bit m)
     int U;
     uint64_t bad_slots;        // invalid slots: id outside [0, Ew) or repeated within its token
     int8_t slot_tab[kMaxSlots][kMaxTokens];  // [unit][token]: the token's slot of the unit's expert, or -1
@@ -93,8 +93,12 @@ __device__ void build_units(Routes &R, uint32_t *emask, int32_t id, int S, int A
         const uint32_t incl = routing::wave_incl_scan_u32(c);
         int pos = (int)(incl - c);
 #pragma unroll
-        for (int j = 0; j < kPer; ++j)
-            if (mk[j]) R.u_exp[pos] = kPer * t + j, R.u_mask[pos] = mk[j], emask[kPer * t + j] = (uint32_t)pos++;
+        for (int j = 0; j < kPer; ++j) {  // branch-free: an expert with no token writes to the sink entry
+            const bool on = mk[j] != 0u;
+            const int at = on ? pos : kMaxSlots;
+            R.u_exp[at] = kPer * t + j, R.u_mask[at] = mk[j], emask[kPer * t + j] = (uint32_t)pos;
+            pos += on ? 1 : 0;
+        }
         if (t == 63) R.U = (int)incl;
         if (t == 0) R.bad_slots = bad_mask;
         if (in && !bad) R.slot_tab[emask[id]][t / A] = (int8_t)t;
@@ -211,6 +215,7 @@ struct FusedSched {
     LayerSync *sync;
     uint32_t *queue;         // this block's work counter (this launch's set)
     int *rnd;                // LDS [4]: the claim (index into the block's queue) of round gr, slot gr & 3
+    int claim_base;          // rounds below it are assigned statically (two a block); the counter numbers the rest
     const uint64_t *tagged;  // the projection's logits as (epoch << 32 | value bits) [M, ld]
     uint32_t epoch;
     uint64_t *trace;  // nullable: this block's stamp slots
@@ -240,7 +245,9 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
         const uint64_t *t1 = fs.tagged + (int64_t)min(wave + kWaves, M - 1) * p.ld;
         const int ecol = p.shared_logit ? p.E : p.E - 1;  // the shared gate's column, or a routed one again
         const uint64_t start = __builtin_amdgcn_s_memrealtime();
+        int polls = 0;
         for (;;) {
+            ++polls;
             bool fresh = true;
             uint64_t a[NV], c[NV];
 #pragma unroll
@@ -263,6 +270,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
             }
             __builtin_amdgcn_s_sleep(1);
         }
+        if (fs.trace && threadIdx.x == 0) fs.trace[2] = __builtin_amdgcn_s_memrealtime(), fs.trace[10] = polls;
     } else {
         routing::load_logits<NV>([&](int e) { return row0[e]; }, p.E, v0);
         routing::load_logits<NV>([&](int e) { return row1[e]; }, p.E, v1);
@@ -288,7 +296,13 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
                                   R.ids + (wave + kWaves) * A, R.coef + (wave + kWaves) * A, nullptr,
                                   lead ? p.router_err : nullptr);
     lds_barrier();
+    if constexpr (FUSED) {
+        if (fs.trace && tid == 0) fs.trace[8] = __builtin_amdgcn_s_memrealtime();
+    }
     build_units(R, emask, tid < S ? R.ids[tid] : 0, S, A, Ew);
+    if constexpr (FUSED) {
+        if (fs.trace && tid == 0) fs.trace[9] = __builtin_amdgcn_s_memrealtime();
+    }
     const int U = __builtin_amdgcn_readfirstlane(R.U);
     const int64_t Nrows = p.N / 2, rowbytes = K / 2, ngroups = K / kSpan;
     if (lead) {
@@ -431,7 +445,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
         constexpr int RS = decltype(slot_tag)::value;
         int claimed = 0;
         if constexpr (FUSED) {  // round gr + 2, claimed while this one streams (written to LDS before the barrier)
-            if (tid == 0) claimed = live(gr + 1) ? (int)claim_one(fs.queue) : kDeadClaim;
+            if (tid == 0) claimed = live(gr + 1) ? fs.claim_base + (int)claim_one(fs.queue) : kDeadClaim;
         }
         uint2 sw[NW], mw[NW];
 #pragma unroll
@@ -490,10 +504,12 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     if constexpr (FUSED) {
         static_assert(!FUSED || (Q > 1 && kRing == 1), "the claims are published at the round's barrier");
         // a live round always issues the next one's loads (clamped when that one is dead): one path for the ring
-        for (int gr = 0;; ++gr) {
+        int gr = 0;
+        for (;; ++gr) {
             consume(gr, std::integral_constant<int, 0>{});
             if (!live(gr + 1)) break;
         }
+        if (fs.trace && tid == 0) fs.trace[11] = gr + 1;
     } else {
         // Runs of kRing rounds, all issuing their loads (an odd count ends with a phantom round that re-loads the
         // last one and stops after its MFMAs): a consume whose loads were conditional would merge two versions of
@@ -805,15 +821,52 @@ __device__ __forceinline__ void project_item(const LayerParams &lp, ProjLds &L, 
             }
         }
     }
+    if constexpr (MT == 8 && kProjRows == 4) {
+        // The wave's 32 sums (row r, token t: value 8 r + t) in 32 exchanges instead of a wave reduction each: every
+        // step pairs lane l with l ^ o and halves the values a lane keeps (the half its bit of o picks), the other
+        // half going to the partner; after o = 32 .. 2 a lane holds one value's sum over its pair of lanes, o = 1
+        // completes it. Value v ends in the lanes l with bits 5..1 of l equal to v.
+        const float *a = &acc[0][0];
+        float hv[16];
+        const bool h5 = (lane >> 5) & 1, h4 = (lane >> 4) & 1, h3 = (lane >> 3) & 1, h2 = (lane >> 2) & 1, h1 = (lane >> 1) & 1;
 #pragma unroll
-    for (int r = 0; r < kProjRows; ++r)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            if (r < nr && t < M) {  // uniform
-                const float s = routing::wave_sum_f32(acc[r][t]);
-                if (lane == 0) L.part[wave][r * kMaxTokens + t] = s;
-            }
+        for (int i = 0; i < 16; ++i) {
+            const float send = h5 ? a[i] : a[16 + i], keep = h5 ? a[16 + i] : a[i];
+            hv[i] = keep + __shfl_xor(send, 32);
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float send = h4 ? hv[i] : hv[8 + i], keep = h4 ? hv[8 + i] : hv[i];
+            hv[i] = keep + __shfl_xor(send, 16);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float send = h3 ? hv[i] : hv[4 + i], keep = h3 ? hv[4 + i] : hv[i];
+            hv[i] = keep + __shfl_xor(send, 8);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float send = h2 ? hv[i] : hv[2 + i], keep = h2 ? hv[2 + i] : hv[i];
+            hv[i] = keep + __shfl_xor(send, 4);
+        }
+        {
+            const float send = h1 ? hv[0] : hv[1], keep = h1 ? hv[1] : hv[0];
+            hv[0] = keep + __shfl_xor(send, 2);
+        }
+        hv[0] += __shfl_xor(hv[0], 1);
+        const int v = (lane >> 1) & 31, r = v >> 3, t = v & 7;
+        if ((lane & 1) == 0 && r < nr && t < M) L.part[wave][r * kMaxTokens + t] = hv[0];
+    } else {
+#pragma unroll
+        for (int r = 0; r < kProjRows; ++r)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                if (r < nr && t < M) {  // uniform
+                    const float s = routing::wave_sum_f32(acc[r][t]);
+                    if (lane == 0) L.part[wave][r * kMaxTokens + t] = s;
+                }
+            }
+    }
     lds_barrier();
     if (tid < nr * kMaxTokens) {
         const int r = tid / kMaxTokens, t = tid % kMaxTokens;
@@ -857,11 +910,19 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerParams lp) {
         if (trace && tid == 0) trace[i] = __builtin_amdgcn_s_memrealtime();
     };
     stamp(0);
-    uint32_t *queue = &sync->queues[lp.epoch & 1][queue_of(b)][0];
-    const FusedSched fs{sync, queue, s_rnd, lp.tagged, lp.epoch, trace, &s_flag};
-    if (tid == 0) {  // the first two gate_up rounds (claims do not depend on the routing)
-        s_rnd[0] = (int)atomicAdd(queue, 1u);
-        s_rnd[1] = (int)atomicAdd(queue, 1u);
+    // The first two gate_up rounds of every block are fixed: the nq blocks sharing queue j (groups of 8 consecutive
+    // blocks g = j, j + kQueues, ..., all full but the grid's last) take rounds r and nq + r, r = the block's rank
+    // among them; the queue's counter then numbers the rounds from 2 nq on. No atomic at the start of the launch
+    // (one would hold up every load issued after it until its turn on the contended counter came).
+    const int grp = b >> 3, qj = grp % kQueues;
+    int nq = 0;
+    for (int g2 = qj; g2 * 8 < G; g2 += kQueues) nq += min(8, G - 8 * g2);
+    uint32_t *queue = &sync->queues[lp.epoch & 1][qj][0];
+    const FusedSched fs{sync, queue, s_rnd, 2 * nq, lp.tagged, lp.epoch, trace, &s_flag};
+    if (tid == 0) {
+        const int r = 8 * (grp / kQueues) + (b & 7);
+        s_rnd[0] = r;
+        s_rnd[1] = nq + r;
     }
     if (b == 0 && tid < kQueues)  // the other set of counters, used by the next launch, starts from zero
         __hip_atomic_store(&sync->queues[(lp.epoch + 1) & 1][tid][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
