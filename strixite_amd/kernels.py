@@ -278,8 +278,9 @@ def topk_workspace_bytes(rows, n_valid, k):
 
 
 def logits_topk(logits, n_valid, k=20, mask=None, ws=None, out=None, nan=None, stream=None):
-    """Per row the best k (value desc, lower id on a tie). Returns (values f32 [rows, k], ids i32 [rows, k], nan)."""
-    rows, ld = logits.shape
+    """Per row the best k (value desc, lower id on a tie) of logits [rows, >= n_valid] (any row stride). Returns
+    (values f32 [rows, k], ids i32 [rows, k], nan, the raw [rows, k, 2] candidates)."""
+    rows, ld = logits.shape[0], logits.stride(0)
     out = torch.empty((rows, k, 2), dtype=torch.int32, device=logits.device) if out is None else out
     nan = torch.empty(rows, dtype=torch.int32, device=logits.device) if nan is None else nan
     if ws is None:
@@ -293,7 +294,7 @@ def logits_topk(logits, n_valid, k=20, mask=None, ws=None, out=None, nan=None, s
 def logits_topk_noalloc(logits, n_valid, k=20, mask=None, out=None, nan=None, stream=None):
     """logits_topk on the library's fixed scratch (sx_logits_topk_noalloc: no workspace, nothing allocated by the
     call). Same returns as logits_topk."""
-    rows, ld = logits.shape
+    rows, ld = logits.shape[0], logits.stride(0)
     out = torch.empty((rows, k, 2), dtype=torch.int32, device=logits.device) if out is None else out
     nan = torch.empty(rows, dtype=torch.int32, device=logits.device) if nan is None else nan
     mw = 0 if mask is None else mask.shape[1]
