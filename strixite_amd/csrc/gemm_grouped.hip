@@ -11,7 +11,7 @@
 //     three steps ahead, each row's sixteen 16-byte chunks XOR-swizzled so that the MFMA operand reads are free of
 //     bank conflicts; the block sums each row's span one step ahead of its use;
 //   - each lane loads its weight rows' codes (32 bytes a row a span) and scales straight into registers, two steps
-//     ahead, and turns a dword of codes into the BF16 operand (128 + code) with four byte selects;
+//     ahead, and turns a dword of codes into the BF16 operand (128 + code) with four byte selects and AND-ORs;
 //   - per span: acc[slot][row] += s[row] * D + (m[row] - 128 s[row]) * sum_span x[slot], with D = the span's
 //     sum x * (128 + code) from the MFMAs, exact in FP32 (the identity qmm uses).
 // MFMA k order: lane half h, MFMA kk, element e of a span <-> code h * 64 + kk * 8 + e (any order A and B share).
@@ -56,14 +56,23 @@ __device__ __forceinline__ int tile_of(unsigned id, int nrb) {
 }
 __device__ __forceinline__ int rowblock_of(unsigned id, int nrb) { return (int)((id % (8u * nrb)) / 8); }
 
-// Operand of 8 codes (one dword: the low nibble of byte b is code 2b) in natural order as BF16 128 + code.
+// (a & b) | c in one ALU operation (the compiler splits the pattern into an AND and an OR).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t d;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
+// Operand of 8 codes (one dword: the low nibble of byte b is code 2b) in natural order as BF16 128 + code: a byte
+// select puts byte b of d (its low nibble wanted) and byte b of d >> 4 (the high nibble) in the two halves, one
+// AND-OR masks the nibbles and sets the exponent: 9 ALU operations for 8 codes.
 __device__ __forceinline__ bf16x8 codes_nat(uint32_t d) {
-    const uint32_t lo = d & 0x0F0F0F0Fu, hi = (d >> 4) & 0x0F0F0F0Fu;
+    const uint32_t hi = d >> 4, m = 0x000F000Fu, e = 0x43004300u;
     uint4 v;
-    v.x = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x43004300u;
-    v.y = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x43004300u;
-    v.z = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x43004300u;
-    v.w = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x43004300u;
+    v.x = and_or(__builtin_amdgcn_perm(hi, d, 0x0C040C00u), m, e);
+    v.y = and_or(__builtin_amdgcn_perm(hi, d, 0x0C050C01u), m, e);
+    v.z = and_or(__builtin_amdgcn_perm(hi, d, 0x0C060C02u), m, e);
+    v.w = and_or(__builtin_amdgcn_perm(hi, d, 0x0C070C03u), m, e);
     return __builtin_bit_cast(bf16x8, v);
 }
 
