@@ -84,7 +84,7 @@ int linear(const char *fn, int bits, const void *x, const sx_qview *w, void *y, 
     if (dks::eligible(bits, w->G, w->N, w->K, M, act, out_act, device_cus())) {  // decode width: K split over a block
         dks::Params d{};
         d.x = x, d.q = w->q, d.scale = w->scale, d.minv = w->minv, d.y = y, d.M = (int)M, d.N = w->N, d.K = w->K;
-        SX_HIP(dks::launch(bits, act, out_act, d, device_cus(), stream_of(stream)), fn);
+        SX_HIP(dks::launch(bits, w->G, act, out_act, d, device_cus(), stream_of(stream)), fn);
         return SX_OK;
     }
     const int nsplit = act == SX_ACT_F32 ? 3 : 1;

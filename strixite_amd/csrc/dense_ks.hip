@@ -1,5 +1,5 @@
 // Dense dequantizing GEMV at decode / verify width (M <= 16 activation rows): y[M, N] = x[M, K] . deq(W)^T for q4
-// (G = 128) and q8 (G = 64), one quantization group a 16-byte-a-lane span (kernels/linear_q4.hpp:26-30,
+// (G = 128 or 64) and q8 (G = 64), one or two quantization groups a 16-byte-a-lane span (kernels/linear_q4.hpp:26-30,
 // kernels/linear_q8.hpp:13-14), for the served shapes (4-64 spans a row) in place of qmm's dense mode (a wave a
 // 16-row tile over the whole K, many tiles a CU in flight at once). A block a CU takes an equal run of the 16-row
 // tiles (to within one tile), and its 8 waves split K Q ways (Q = min(8, spans / 4)) and work on 8 / Q tiles at a
@@ -9,6 +9,9 @@
 // with their span sums; each span folds as acc += s * D + (m - off * s) * sum x with D from
 // v_mfma_f32_16x16x32_bf16 on (off + code). The Q partial 16 x 16 tiles of a tile meet in LDS after a barrier (Q > 1),
 // are summed in K order and stored by the Q waves that made them (a quarter-tile or less each).
+// q4 G = 64 (the MTP draft head) has two groups a span: a span's lanes 0-31 hold the first group's codes and lanes
+// 32-63 the second's, so each MFMA runs twice, once with the other group's lanes reading a zero row of the activation
+// planes instead of the activations (no ALU selects), and each group folds with its own scale, min and x sums.
 #include "dense_ks.hpp"
 #include "qmm_impl.hpp"
 
@@ -27,12 +30,22 @@ constexpr int kSpanBytes = 64;  // a row's span: 16 bytes a lane, 4 lanes
 constexpr int kRingKs = 1;
 template <int SPW> constexpr int kLagKs = SPW == 8 ? 6 : 2;
 
-// The BF16 word of span s in a window of 4 (uint2) or 8 (uint4) scales / mins.
+// The dword holding BF16 word s of a window of 4 (uint2), 8 (uint4) or 16 (Win16) scales / mins.
+struct Win16 {
+    uint4 a, b;
+};
 __device__ __forceinline__ uint32_t win_word(const uint2 &w, int s) { return s < 2 ? w.x : w.y; }
 __device__ __forceinline__ uint32_t win_word(const uint4 &w, int s) { return qmm::detail::dword(w, s >> 1); }
+__device__ __forceinline__ uint32_t win_word(const Win16 &w, int s) {
+    return s < 8 ? qmm::detail::dword(w.a, s >> 1) : qmm::detail::dword(w.b, (s - 8) >> 1);
+}
+__device__ __forceinline__ float win_value(uint32_t dw, int s) {
+    return __uint_as_float((s & 1) ? (dw & 0xFFFF0000u) : (dw << 16));
+}
 
-template <int BITS, int NPL, int SPW, typename TX, typename TY>
+template <int BITS, int NPL, int SPW, int GS, typename TX, typename TY>
 __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
+    static_assert(GS == 1 || (GS == 2 && BITS == 4), "two groups a span: q4 G = 64");
     using F = qmm::detail::Fmt<BITS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     __shared__ __attribute__((aligned(16))) float red[2][kWaves][4][64];  // [round & 1][wave][v][lane]
@@ -44,8 +57,9 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     const int64_t K = p.K, N = p.N, ldx = K + 8;
     const int nspan = (int)(K / F::kSpanCodes), chunks8 = (int)(K / 8), lg_chunks = __builtin_ctz((unsigned)chunks8);
     const int n16 = lane & 15, g = lane >> 4;
-    uint16_t *xs = reinterpret_cast<uint16_t *>(smem);                      // [NPL][M][K + 8]
-    float *xsum = reinterpret_cast<float *>(smem + (size_t)NPL * M * ldx * 2);  // [nspan][16]
+    const int MP = GS == 2 ? M + 1 : M;  // rows a plane (GS = 2: row M is zeros)
+    uint16_t *xs = reinterpret_cast<uint16_t *>(smem);                       // [NPL][MP][K + 8]
+    float *xsum = reinterpret_cast<float *>(smem + (size_t)NPL * MP * ldx * 2);  // [nspan * GS][16]
 
     // this block's tiles [b0, b1), in rounds of P
     const int64_t T16 = (N + 15) / 16;
@@ -54,8 +68,8 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
 
     // weight ring: round r = the slice kq of tile b0 + r P + ip (clamped into the run: a clamped round loads a
     // valid tile and stores nothing); the round's scales / mins as one window of SPW BF16 a row
-    using Win = std::conditional_t<SPW == 4, uint2, uint4>;
-    const int64_t rowbytes = K * BITS / 8, ngroups = nspan;
+    using Win = std::conditional_t<SPW * GS == 4, uint2, std::conditional_t<SPW * GS == 8, uint4, Win16>>;
+    const int64_t rowbytes = K * BITS / 8, ngroups = (int64_t)nspan * GS;
     uint4 ring[kRingKs][SPW];
     Win sw_n[kRingKs], mw_n[kRingKs];
     int ii = 0;
@@ -65,8 +79,8 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
         const int tile = min(b0 + ii * P + ip, b1 - 1);
         const int64_t n = (int64_t)tile * 16 + n16, row = n < N ? n : N - 1;
         iq = p.q + row * rowbytes + (int64_t)kq * SPW * kSpanBytes + g * 16;
-        is_ = p.scale + row * ngroups + kq * SPW;
-        im = p.minv + row * ngroups + kq * SPW;
+        is_ = p.scale + row * ngroups + kq * SPW * GS;
+        im = p.minv + row * ngroups + kq * SPW * GS;
     };
     auto advance_issue = [&]() {
         ++ii;
@@ -104,10 +118,10 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
                 qmm::detail::chunk_planes<BITS, NPL, TX>(raw[b], planes, sum);
 #pragma unroll
                 for (int s = 0; s < NPL; ++s)
-                    *reinterpret_cast<uint4 *>(xs + ((int64_t)s * M + r) * ldx + (int64_t)c8 * 8) = planes[s];
-                constexpr int CPS = F::kSpanCodes / 8;  // chunks a span
-                sum = qmm::detail::group_sum_c<CPS>(sum);
-                if ((c8 & (CPS - 1)) == 0) xsum[(c8 / CPS) * 16 + r] = sum;
+                    *reinterpret_cast<uint4 *>(xs + ((int64_t)s * MP + r) * ldx + (int64_t)c8 * 8) = planes[s];
+                constexpr int CPG = F::kSpanCodes / 8 / GS;  // chunks a group
+                sum = qmm::detail::group_sum_c<CPG>(sum);
+                if ((c8 & (CPG - 1)) == 0) xsum[(c8 / CPG) * 16 + r] = sum;
             }
         }
     };
@@ -129,15 +143,24 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
         if (base + kStage * kThreads >= n_items_x) break;
         load_x(base + kStage * kThreads);
     }
-    for (int i = tid; i < nspan * 16; i += kThreads)
+    for (int i = tid; i < nspan * GS * 16; i += kThreads)
         if ((i & 15) >= M) xsum[i] = 0.f;
+    if constexpr (GS == 2)  // the zero row of each plane
+        for (int i = tid; i < NPL * (int)(ldx / 8); i += kThreads)
+            *reinterpret_cast<uint4 *>(xs + ((int64_t)(i / (ldx / 8)) * MP + M) * ldx + (int64_t)(i % (ldx / 8)) * 8) =
+                uint4{0u, 0u, 0u, 0u};
     __syncthreads();
     if (groups <= 0) return;
 
     // 2. consume: A rows = activation rows (lane row n16, zeros past M), D rows 4g .. 4g + 3, columns = the tile's rows
     const bool a_on = n16 < M;
-    const uint16_t *a_row = xs + (int64_t)(a_on ? n16 : 0) * ldx + g * (F::kSpanCodes / 4) + (int64_t)kq * SPW * F::kSpanCodes;
-    const float *xsg = xsum + kq * SPW * 16 + 4 * g;
+    const int64_t a_col = g * (F::kSpanCodes / 4) + (int64_t)kq * SPW * F::kSpanCodes;
+    const uint16_t *a_row = xs + (int64_t)(a_on ? n16 : 0) * ldx + a_col;
+    // GS = 2: group 0's MFMAs read the activations on lanes 0-31 (its codes) and the zero row on lanes 32-63; group
+    // 1's the other way round
+    const uint16_t *a_zero = xs + (int64_t)M * ldx + a_col;
+    const uint16_t *a_g0 = g < 2 ? a_row : a_zero, *a_g1 = g < 2 ? a_zero : a_row;
+    const float *xsg = xsum + kq * SPW * GS * 16 + 4 * g;
     // the D rows 4 g + vb .. whose results this wave stores (Q = 8: on half the lanes)
     const int VS = Q >= 4 ? 1 : 4 / Q;
     const int vb = Q == 8 ? kq >> 1 : kq * VS;
@@ -159,24 +182,35 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
 #pragma unroll
             for (int t = 0; t < F::kMfmas; ++t) bop[t] = qmm::detail::codes_b<BITS>(ring[RS][s], t);
             if (s >= kLagKs<SPW>) issue_slot(ring[RS], s - kLagKs<SPW>);
-            f32x4 D = f32x4{0.f, 0.f, 0.f, 0.f};
+            f32x4 D[GS];
+#pragma unroll
+            for (int h = 0; h < GS; ++h) D[h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int pl = 0; pl < NPL; ++pl)
 #pragma unroll
                 for (int t = 0; t < F::kMfmas; ++t) {
-                    const bf16x8 av = a_on ? *reinterpret_cast<const bf16x8 *>(a_row + (int64_t)pl * M * ldx + s * F::kSpanCodes + t * 8)
-                                           : bf16x8{};
-                    D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bop[t], D, 0, 0, 0);
+                    const int64_t o = (int64_t)pl * MP * ldx + s * F::kSpanCodes + t * 8;
+                    if constexpr (GS == 1) {
+                        const bf16x8 av = a_on ? *reinterpret_cast<const bf16x8 *>(a_row + o) : bf16x8{};
+                        D[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bop[t], D[0], 0, 0, 0);
+                    } else {
+                        const bf16x8 a0 = a_on ? *reinterpret_cast<const bf16x8 *>(a_g0 + o) : bf16x8{};
+                        const bf16x8 a1 = a_on ? *reinterpret_cast<const bf16x8 *>(a_g1 + o) : bf16x8{};
+                        D[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bop[t], D[0], 0, 0, 0);
+                        D[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bop[t], D[1], 0, 0, 0);
+                    }
                 }
-            const float4 xv = *reinterpret_cast<const float4 *>(xsg + s * 16);
-            const uint32_t swd = win_word(sw, s), mwd = win_word(mw, s);
-            const float s_ = __uint_as_float((s & 1) ? (swd & 0xFFFF0000u) : (swd << 16));
-            const float m_ = __uint_as_float((s & 1) ? (mwd & 0xFFFF0000u) : (mwd << 16));
-            const float cm = fmaf(-F::kOff, s_, m_);
-            acc[0] = fmaf(s_, D[0], fmaf(cm, xv.x, acc[0]));
-            acc[1] = fmaf(s_, D[1], fmaf(cm, xv.y, acc[1]));
-            acc[2] = fmaf(s_, D[2], fmaf(cm, xv.z, acc[2]));
-            acc[3] = fmaf(s_, D[3], fmaf(cm, xv.w, acc[3]));
+#pragma unroll
+            for (int h = 0; h < GS; ++h) {
+                const int gi = s * GS + h;  // the group's index in the window
+                const float4 xv = *reinterpret_cast<const float4 *>(xsg + gi * 16);
+                const float s_ = win_value(win_word(sw, gi), gi), m_ = win_value(win_word(mw, gi), gi);
+                const float cm = fmaf(-F::kOff, s_, m_);
+                acc[0] = fmaf(s_, D[h][0], fmaf(cm, xv.x, acc[0]));
+                acc[1] = fmaf(s_, D[h][1], fmaf(cm, xv.y, acc[1]));
+                acc[2] = fmaf(s_, D[h][2], fmaf(cm, xv.z, acc[2]));
+                acc[3] = fmaf(s_, D[h][3], fmaf(cm, xv.w, acc[3]));
+            }
         }
 #pragma unroll
         for (int s = SPW - kLagKs<SPW>; s < SPW; ++s) issue_slot(ring[RS], s);
@@ -212,9 +246,9 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave exits
 }
 
-template <int BITS, int NPL, int SPW, typename TX, typename TY>
+template <int BITS, int NPL, int SPW, int GS, typename TX, typename TY>
 hipError_t go(const Params &p, int cus, size_t lds, hipStream_t stream) {
-    auto fn = dense_ks_kernel<BITS, NPL, SPW, TX, TY>;
+    auto fn = dense_ks_kernel<BITS, NPL, SPW, GS, TX, TY>;
     // the dynamic LDS limit, set once an instantiation (every launch asks for <= kLdsMax; setting it twice from two
     // threads is harmless)
     static std::atomic<bool> sized{false};
@@ -230,15 +264,15 @@ hipError_t go(const Params &p, int cus, size_t lds, hipStream_t stream) {
 
 }  // namespace
 
-size_t lds_bytes(int act, int64_t M, int64_t K, int bits) {
+size_t lds_bytes(int act, int64_t M, int64_t K, int bits, int64_t G) {
     const int npl = act == SX_ACT_F32 ? 3 : 1;
-    const int64_t nspan = K / (bits == 4 ? 128 : 64);
-    return (size_t)npl * M * (K + 8) * 2 + (size_t)nspan * 16 * 4;
+    const int64_t span = bits == 4 ? 128 : 64, nspan = K / span, gs = span / G;
+    return (size_t)npl * (M + (gs == 2 ? 1 : 0)) * (K + 8) * 2 + (size_t)nspan * gs * 16 * 4;
 }
 
 bool eligible(int bits, int64_t G, int64_t N, int64_t K, int64_t M, int act, int out_act, int cus) {
     (void)N, (void)cus;  // any number of tiles: a block takes a run of them
-    if (!((bits == 4 && G == 128) || (bits == 8 && G == 64))) return false;
+    if (!((bits == 4 && (G == 128 || G == 64)) || (bits == 8 && G == 64))) return false;
     const int64_t span = bits == 4 ? 128 : 64;
     if (K % span != 0) return false;
     const int64_t nspan = K / span;
@@ -247,27 +281,34 @@ bool eligible(int bits, int64_t G, int64_t N, int64_t K, int64_t M, int act, int
     if (!((act == SX_ACT_BF16 && (out_act == SX_ACT_BF16 || out_act == SX_ACT_F32)) ||
           (act == SX_ACT_F32 && out_act == SX_ACT_F32)))
         return false;
-    return lds_bytes(act, M, K, bits) <= kLdsMax;
+    return lds_bytes(act, M, K, bits, G) <= kLdsMax;
 }
 
-hipError_t launch(int bits, int act, int out_act, const Params &p0, int cus, hipStream_t stream) {
+hipError_t launch(int bits, int64_t G, int act, int out_act, const Params &p0, int cus, hipStream_t stream) {
     Params p = p0;
     const int64_t nspan = p.K / (bits == 4 ? 128 : 64);
-    p.Q = (int)(nspan / 4 < kWaves ? nspan / 4 : kWaves);
+    // 8 spans (8 KB) a wave a round when a block has at least two tiles for each round's 8 / Q tile lanes (the MTP
+    // draft head: 49 against 51 us), else 4 spans a wave
+    const int64_t tiles_per_block = ((p.N + 15) / 16 + cus - 1) / cus;
+    const int64_t q8 = nspan / 8 < kWaves ? nspan / 8 : kWaves;
+    if (nspan >= 8 && tiles_per_block >= 2 * (kWaves / q8)) p.Q = (int)q8;
+    else p.Q = (int)(nspan / 4 < kWaves ? nspan / 4 : kWaves);
     const int spw = (int)(nspan / p.Q);
-    const size_t lds = lds_bytes(act, p.M, p.K, bits);
-    auto by_spw = [&](auto bits_tag, auto npl_tag, auto tx, auto ty) {
-        constexpr int B = decltype(bits_tag)::value, NPL = decltype(npl_tag)::value;
+    const size_t lds = lds_bytes(act, p.M, p.K, bits, G);
+    auto by_spw = [&](auto bits_tag, auto gs_tag, auto npl_tag, auto tx, auto ty) {
+        constexpr int B = decltype(bits_tag)::value, GS = decltype(gs_tag)::value, NPL = decltype(npl_tag)::value;
         using TX = decltype(tx);
         using TY = decltype(ty);
-        return spw == 4 ? go<B, NPL, 4, TX, TY>(p, cus, lds, stream) : go<B, NPL, 8, TX, TY>(p, cus, lds, stream);
+        return spw == 4 ? go<B, NPL, 4, GS, TX, TY>(p, cus, lds, stream) : go<B, NPL, 8, GS, TX, TY>(p, cus, lds, stream);
     };
-    auto by_act = [&](auto bits_tag) {
-        if (act == SX_ACT_F32) return by_spw(bits_tag, std::integral_constant<int, 3>{}, float{}, float{});
-        if (out_act == SX_ACT_F32) return by_spw(bits_tag, std::integral_constant<int, 1>{}, uint16_t{}, float{});
-        return by_spw(bits_tag, std::integral_constant<int, 1>{}, uint16_t{}, uint16_t{});
+    auto by_act = [&](auto bits_tag, auto gs_tag) {
+        if (act == SX_ACT_F32) return by_spw(bits_tag, gs_tag, std::integral_constant<int, 3>{}, float{}, float{});
+        if (out_act == SX_ACT_F32) return by_spw(bits_tag, gs_tag, std::integral_constant<int, 1>{}, uint16_t{}, float{});
+        return by_spw(bits_tag, gs_tag, std::integral_constant<int, 1>{}, uint16_t{}, uint16_t{});
     };
-    return bits == 4 ? by_act(std::integral_constant<int, 4>{}) : by_act(std::integral_constant<int, 8>{});
+    if (bits == 8) return by_act(std::integral_constant<int, 8>{}, std::integral_constant<int, 1>{});
+    if (G == 64) return by_act(std::integral_constant<int, 4>{}, std::integral_constant<int, 2>{});
+    return by_act(std::integral_constant<int, 4>{}, std::integral_constant<int, 1>{});
 }
 
 }  // namespace sx::dks

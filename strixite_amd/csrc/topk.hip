@@ -259,21 +259,61 @@ __device__ __forceinline__ Top2 top2_xor(const Top2 &p, int off) {
             (uint32_t)__shfl_xor((int)p.nan, off)};
 }
 
+// One value into a thread's running top-2 (indices offered in ascending order: the strict > keeps the lower index of
+// equal values).
+__device__ __forceinline__ void top2_take(Top2 &p, float v, int64_t i) {
+    if (v != v) {
+        p.nan = 1u;
+        return;
+    }
+    if (p.i1 == INT_MAX || v > p.b1) p.b2 = p.b1, p.b1 = v, p.i1 = (int)i;
+    else if (v > p.b2) p.b2 = v;
+}
+
+// VEC: 16-byte loads (n % 4 == 0, x 16-byte aligned), thread t taking elements 4j .. 4j + 3 for j = t, t + 1024, ...
+// Either way a thread's indices ascend, and its loads go out in batches of kPickBatch before any is used (the index
+// clamped into the row).
+template <bool VEC>
 __global__ void __launch_bounds__(kPickThreads)
     mtp_pick_kernel(const float *x, int64_t n, const uint32_t *router_err, const uint32_t *expert_err,
                     const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out) {
     __shared__ Top2 part[kPickThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     Top2 p{-INFINITY, -INFINITY, INT_MAX, 0u};
-    // A thread's indices ascend, so the strict > keeps the lower index of equal values.
-    for (int64_t i = tid; i < n; i += kPickThreads) {
-        const float v = x[i];
-        if (v != v) {
-            p.nan = 1u;
-            continue;
+    constexpr int kPickBatch = 16;
+    if constexpr (VEC) {
+        const int64_t n4 = n / 4;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        for (int64_t base = tid; base < n4; base += (int64_t)kPickBatch * kPickThreads) {
+            float4 v[kPickBatch];
+#pragma unroll
+            for (int b = 0; b < kPickBatch; ++b) {
+                const int64_t j = base + (int64_t)b * kPickThreads;
+                v[b] = x4[j < n4 ? j : n4 - 1];
+            }
+#pragma unroll
+            for (int b = 0; b < kPickBatch; ++b) {
+                const int64_t j = base + (int64_t)b * kPickThreads;
+                if (j >= n4) break;
+                top2_take(p, v[b].x, 4 * j), top2_take(p, v[b].y, 4 * j + 1);
+                top2_take(p, v[b].z, 4 * j + 2), top2_take(p, v[b].w, 4 * j + 3);
+            }
         }
-        if (p.i1 == INT_MAX || v > p.b1) p.b2 = p.b1, p.b1 = v, p.i1 = (int)i;
-        else if (v > p.b2) p.b2 = v;
+    } else {
+        for (int64_t base = tid; base < n; base += (int64_t)kPickBatch * kPickThreads) {
+            float v[kPickBatch];
+#pragma unroll
+            for (int b = 0; b < kPickBatch; ++b) {
+                const int64_t i = base + (int64_t)b * kPickThreads;
+                v[b] = x[i < n ? i : n - 1];
+            }
+#pragma unroll
+            for (int b = 0; b < kPickBatch; ++b) {
+                const int64_t i = base + (int64_t)b * kPickThreads;
+                if (i >= n) break;
+                top2_take(p, v[b], i);
+            }
+        }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) p = top2_merge(p, top2_xor(p, off));
@@ -482,8 +522,12 @@ int sx_mtp_pick(const float *logits, int64_t n, const uint32_t *router_err, cons
                 const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out, sx_stream stream) {
     SX_CHECK(logits && router_err && expert_err && attn_err && emb_err && out, "null pointer");
     SX_CHECK(n >= 1 && n <= INT_MAX, "n = ", n, " logits, expected 1..", INT_MAX);
-    mtp_pick_kernel<<<1, kPickThreads, 0, stream_of(stream)>>>(logits, n, router_err, expert_err, attn_err, emb_err,
-                                                              out);
+    if (n % 4 == 0 && aligned(logits, 16))
+        mtp_pick_kernel<true><<<1, kPickThreads, 0, stream_of(stream)>>>(logits, n, router_err, expert_err, attn_err,
+                                                                        emb_err, out);
+    else
+        mtp_pick_kernel<false><<<1, kPickThreads, 0, stream_of(stream)>>>(logits, n, router_err, expert_err, attn_err,
+                                                                         emb_err, out);
     SX_LAUNCHED("mtp_pick n=", n);
     return SX_OK;
 }
