@@ -38,6 +38,8 @@ def parse():
                          "config-3 gate_up and down kernels alone, and exit")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only config 4's prefill layer (for rocprofv3 runs): one JSON line with its timings")
+    ap.add_argument("--draft-only", action="store_true",
+                    help="only the MTP draft head (for rocprofv3 runs): one JSON line with its timings")
     ap.add_argument("--tail-only", action="store_true",
                     help="only config 5's verify tail (for rocprofv3 runs): one JSON line with its timings")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -507,6 +509,9 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps({"cfg4_prefill_layer": prefill_layer()}))
+        return
+    if args.draft_only:
+        print(json.dumps({"mtp_draft_head": draft_head()}))
         return
     if args.tail_only:
         print(json.dumps({"cfg5_verify_tail": verify_tail()}))
