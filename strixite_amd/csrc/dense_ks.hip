@@ -9,9 +9,11 @@
 // with their span sums; each span folds as acc += s * D + (m - off * s) * sum x with D from
 // v_mfma_f32_16x16x32_bf16 on (off + code). The Q partial 16 x 16 tiles of a tile meet in LDS after a barrier (Q > 1),
 // are summed in K order and stored by the Q waves that made them (a quarter-tile or less each).
+// Each plane has a zero row after the M activation rows: the A-operand lanes past M read it, so every A read is an
+// unconditional LDS load (a select of the read against zeros made each read wait for the one before it).
 // q4 G = 64 (the MTP draft head) has two groups a span: a span's lanes 0-31 hold the first group's codes and lanes
-// 32-63 the second's, so each MFMA runs twice, once with the other group's lanes reading a zero row of the activation
-// planes instead of the activations (no ALU selects), and each group folds with its own scale, min and x sums.
+// 32-63 the second's, so each MFMA runs twice, once with the other group's lanes reading the zero row instead of the
+// activations (no ALU selects), and each group folds with its own scale, min and x sums.
 #include "dense_ks.hpp"
 #include "qmm_impl.hpp"
 
@@ -57,7 +59,7 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     const int64_t K = p.K, N = p.N, ldx = K + 8;
     const int nspan = (int)(K / F::kSpanCodes), chunks8 = (int)(K / 8), lg_chunks = __builtin_ctz((unsigned)chunks8);
     const int n16 = lane & 15, g = lane >> 4;
-    const int MP = GS == 2 ? M + 1 : M;  // rows a plane (GS = 2: row M is zeros)
+    const int MP = M + 1;  // rows a plane (row M: zeros)
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);                       // [NPL][MP][K + 8]
     float *xsum = reinterpret_cast<float *>(smem + (size_t)NPL * MP * ldx * 2);  // [nspan * GS][16]
 
@@ -145,20 +147,19 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     }
     for (int i = tid; i < nspan * GS * 16; i += kThreads)
         if ((i & 15) >= M) xsum[i] = 0.f;
-    if constexpr (GS == 2)  // the zero row of each plane
-        for (int i = tid; i < NPL * (int)(ldx / 8); i += kThreads)
-            *reinterpret_cast<uint4 *>(xs + ((int64_t)(i / (ldx / 8)) * MP + M) * ldx + (int64_t)(i % (ldx / 8)) * 8) =
-                uint4{0u, 0u, 0u, 0u};
+    for (int i = tid; i < NPL * (int)(ldx / 8); i += kThreads)  // the zero row of each plane
+        *reinterpret_cast<uint4 *>(xs + ((int64_t)(i / (ldx / 8)) * MP + M) * ldx + (int64_t)(i % (ldx / 8)) * 8) =
+            uint4{0u, 0u, 0u, 0u};
     __syncthreads();
     if (groups <= 0) return;
 
     // 2. consume: A rows = activation rows (lane row n16, zeros past M), D rows 4g .. 4g + 3, columns = the tile's rows
     const bool a_on = n16 < M;
     const int64_t a_col = g * (F::kSpanCodes / 4) + (int64_t)kq * SPW * F::kSpanCodes;
-    const uint16_t *a_row = xs + (int64_t)(a_on ? n16 : 0) * ldx + a_col;
+    const uint16_t *a_zero = xs + (int64_t)M * ldx + a_col;
+    const uint16_t *a_row = a_on ? xs + (int64_t)n16 * ldx + a_col : a_zero;
     // GS = 2: group 0's MFMAs read the activations on lanes 0-31 (its codes) and the zero row on lanes 32-63; group
     // 1's the other way round
-    const uint16_t *a_zero = xs + (int64_t)M * ldx + a_col;
     const uint16_t *a_g0 = g < 2 ? a_row : a_zero, *a_g1 = g < 2 ? a_zero : a_row;
     const float *xsg = xsum + kq * SPW * GS * 16 + 4 * g;
     // the D rows 4 g + vb .. whose results this wave stores (Q = 8: on half the lanes)
@@ -191,11 +192,11 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
                 for (int t = 0; t < F::kMfmas; ++t) {
                     const int64_t o = (int64_t)pl * MP * ldx + s * F::kSpanCodes + t * 8;
                     if constexpr (GS == 1) {
-                        const bf16x8 av = a_on ? *reinterpret_cast<const bf16x8 *>(a_row + o) : bf16x8{};
+                        const bf16x8 av = *reinterpret_cast<const bf16x8 *>(a_row + o);
                         D[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bop[t], D[0], 0, 0, 0);
                     } else {
-                        const bf16x8 a0 = a_on ? *reinterpret_cast<const bf16x8 *>(a_g0 + o) : bf16x8{};
-                        const bf16x8 a1 = a_on ? *reinterpret_cast<const bf16x8 *>(a_g1 + o) : bf16x8{};
+                        const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(a_g0 + o);
+                        const bf16x8 a1 = *reinterpret_cast<const bf16x8 *>(a_g1 + o);
                         D[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bop[t], D[0], 0, 0, 0);
                         D[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bop[t], D[1], 0, 0, 0);
                     }
@@ -267,7 +268,7 @@ hipError_t go(const Params &p, int cus, size_t lds, hipStream_t stream) {
 size_t lds_bytes(int act, int64_t M, int64_t K, int bits, int64_t G) {
     const int npl = act == SX_ACT_F32 ? 3 : 1;
     const int64_t span = bits == 4 ? 128 : 64, nspan = K / span, gs = span / G;
-    return (size_t)npl * (M + (gs == 2 ? 1 : 0)) * (K + 8) * 2 + (size_t)nspan * gs * 16 * 4;
+    return (size_t)npl * (M + 1) * (K + 8) * 2 + (size_t)nspan * gs * 16 * 4;
 }
 
 bool eligible(int bits, int64_t G, int64_t N, int64_t K, int64_t M, int act, int out_act, int cus) {
