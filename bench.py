@@ -164,10 +164,11 @@ def moe_layer_bench(args, out):
     ids_b = torch.empty((M, k), dtype=torch.int32, device="cuda")
     coef_b = torch.empty((M, k), dtype=torch.float32, device="cuda")
     rerr, eerr = torch.zeros(4, dtype=torch.int32, device="cuda"), torch.zeros(4, dtype=torch.int32, device="cuda")
+    gsync = kx.verify_layer_sync()  # the pool, as the layer's own launch uses it
 
     def gate_up(i):
         kx.verify_gate_up(xs[i % R], routes[i % R][3], gu, E, k, ids=ids_b, coef=coef_b, h=h, router_err=rerr,
-                          expert_err=eerr, h_sums=h_sums)
+                          expert_err=eerr, h_sums=h_sums, sync=gsync)
 
     ms = time_window(gate_up)
     gu_bytes = sum(gate_up_bytes(Us[r], gu_per_expert, M, d, E, k, I) for r in range(R)) / R
@@ -443,9 +444,10 @@ def probe():
     ids_b = torch.empty((M, k), dtype=torch.int32, device="cuda")
     coef_b = torch.empty((M, k), dtype=torch.float32, device="cuda")
     yb = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
+    gsync = kx.verify_layer_sync()
     torch.cuda.synchronize()
     for i in range(R):
-        kx.verify_gate_up(xs[i], routes[i][2], gu, E, k, ids=ids_b, coef=coef_b, h=h, h_sums=h_sums)
+        kx.verify_gate_up(xs[i], routes[i][2], gu, E, k, ids=ids_b, coef=coef_b, h=h, h_sums=h_sums, sync=gsync)
     for i in range(R):
         kx.verify_down(h, dn, routes[i][0], routes[i][1], E, y=yb, h_sums=h_sums)
     torch.cuda.synchronize()

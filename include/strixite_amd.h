@@ -103,11 +103,15 @@ int sx_moe_verify_supported(int64_t M, int64_t A, int64_t E, int64_t k, int64_t 
                             const sx_qview *down, int act);
 /* route (ids, coef [M, A]; router_err) + h [M, A, I] = silu(x W_gate^T) * (x W_up^T) per slot (expert_err, NaN rows
  * for invalid slots). shared_logit nullable. h_sums (nullable, 16-byte aligned): FP32 [M * A, ceil(I / 16)], the sum
- * of each 16-feature run of the valid slots' h rows as stored, for sx_moe_verify_down. */
+ * of each 16-feature run of the valid slots' h rows as stored, for sx_moe_verify_down. sync (nullable): a buffer of
+ * sx_moe_verify_layer_sync_bytes bytes as sx_moe_verify_layer takes it (zeroed once, one per stream, may be the same
+ * buffer): with K = 4096 each compute unit then streams a fixed run of about 4/5 of an equal share of the weight
+ * tiles and takes the rest from a shared pool, so faster ones take more (without it each takes a fixed equal
+ * share); the outputs are the same either way. */
 int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
                           const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *gate_up,
                           int64_t Ew, int32_t *ids, float *coef, void *h, float *h_sums, int act,
-                          uint32_t *router_err, uint32_t *expert_err, sx_stream stream);
+                          uint32_t *router_err, uint32_t *expert_err, void *sync, sx_stream stream);
 /* y [M, N] = sum_a coef[m, a] * (h[m, a] W_down[ids[m, a]]^T); NaN rows for tokens with an invalid slot. h_sums
  * (nullable): the h_sums sx_moe_verify_gate_up wrote with this h (saves the kernel summing h itself). */
 int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A, const int32_t *ids,

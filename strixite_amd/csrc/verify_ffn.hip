@@ -133,10 +133,12 @@ __device__ __forceinline__ uint4 load16_agent(const void *base, uint32_t bytes, 
     return uint4{v[0], v[1], v[2], v[3]};
 }
 
-// The gate_up phase's work queue of a block: blocks 8j .. 8j + 7 (one on each XCD under the round-robin dispatch)
-// share queue j mod kQueues, so every queue is served by the same mix of XCDs and the queues drain together.
+// The gate_up pool of a block: blocks 8j .. 8j + 7 (one on each XCD under the round-robin dispatch) share part
+// j mod kQueues, so every part is served by the same mix of XCDs and the parts drain together.
 __device__ __forceinline__ int queue_of(int block) { return (block >> 3) % kQueues; }
-constexpr int kDeadClaim = 1 << 24;  // a claim past every queue (the block's work is done)
+constexpr int kDeadClaim = 1 << 24;  // a claim past the pool (the block's work is done)
+// The share of the gate_up items taken in fixed runs (the rest from the shared pool): kFixedNum / kFixedDen.
+constexpr int kFixedNum = 4, kFixedDen = 5;
 
 // One claim from a work counter by the calling lane. The zero offset comes from asm so the compiler cannot see
 // that every lane names one address: it would otherwise merge the lanes' atomics into one and read its result out
@@ -196,10 +198,13 @@ __device__ bool block_wait(const uint32_t *flags, int n, uint32_t epoch, uint32_
 // registers as MFMA A operands (code order) for the whole kernel, with their span sums.
 //
 // FUSED (the one-launch layer): the logits come from the projection phase (agent-scope loads of the tagged pairs),
-// h and its sums are stored at agent scope for the down phase of every block, and the items come from one of
-// kQueues work queues (contiguous runs of the items, each shared by blocks spread over every XCD) one round at a
-// time, claimed two rounds ahead: a block that streams faster takes more rounds, so the blocks finish within about
-// a round of each other however unevenly the memory system serves them.
+// h and its sums are stored at agent scope for the down phase of every block.
+// DYN (the one-launch layer; gate_up with a sync buffer): a block streams a fixed run of S0 items first (S0 = about
+// 4/5 of an equal share: a run of adjacent tiles streams faster than tiles taken one by one), then items from the
+// pool after all the runs, one round at a time from its part of the pool (kQueues parts, each shared by blocks on
+// every XCD): its first two fixed, the rest claimed from the part's counter two rounds ahead. A block that streams
+// faster takes more of the pool, so the blocks finish within about a round of each other however unevenly the
+// memory system serves them.
 struct GuLds {
     float red[2][kWaves][2][4][64];  // [round & 1][wave][gate, up][v][lane]
 };
@@ -213,16 +218,15 @@ struct DnLds {
 
 struct FusedSched {
     LayerSync *sync;
-    uint32_t *queue;         // this block's work counter (this launch's set)
-    int *rnd;                // LDS [4]: the claim (index into the block's queue) of round gr, slot gr & 3
-    int claim_base;          // rounds below it are assigned statically (two a block); the counter numbers the rest
+    uint32_t *queue;         // the counter of the block's part of the pool (this launch's set)
+    int *rnd;                // LDS [4]: the claim (index into the part) of round gr, slot gr & 3
     const uint64_t *tagged;  // the projection's logits as (epoch << 32 | value bits) [M, ld]
     uint32_t epoch;
     uint64_t *trace;  // nullable: this block's stamp slots
     int *flag;        // LDS scratch of block_wait
 };
 
-template <int NV, int Q, bool FUSED>
+template <int NV, int Q, bool FUSED, bool DYN = FUSED>
 __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Routes &R, uint32_t *emask,
                                             const FusedSched &fs) {
     constexpr int P = kWaves / Q;  // items a round
@@ -319,19 +323,32 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
         }
     }
 
-    // 3. the items of U x T16 (expert-major). Standalone: this block's run [b0, b1) in rounds of P. FUSED: rounds of
-    // one item (Q = 8) claimed from the queue [b0, b1) of this block (fs.rnd[gr & 3] = the claim of round gr)
+    // 3. the items of U x T16 (expert-major). Static: this block's run [b0, b1) in rounds of P. DYN: rounds of one
+    // item (Q = 8), rounds gr < S0 from the run [blk S0, blk S0 + S0), then items q0 + j of the block's part
+    // [q0, q1) of the pool [G S0, F): j = r and nq + r for the first two (r: the block's rank among the nq blocks of
+    // the part), then the claims in fs.rnd[gr & 3], from 2 nq on
     const int T16 = (int)((Nrows + 15) / 16);
     const int64_t F = (int64_t)U * T16;
-    const int part = FUSED ? queue_of(blockIdx.x) : (int)blockIdx.x, parts = FUSED ? kQueues : (int)gridDim.x;
-    const int b0 = (int)(part * F / parts), b1 = (int)((part + 1) * F / parts);
-    const int groups = FUSED ? 0 : (b1 - b0 + P - 1) / P;  // rounds (block-uniform; standalone)
+    const int G = (int)gridDim.x, blk = (int)blockIdx.x;
+    const int S0 = DYN ? (int)(F * kFixedNum / kFixedDen / G) : 0;
+    const int64_t PF = F - (int64_t)G * S0;  // the pool
+    const int qj = queue_of(blk), grp = blk >> 3;
+    const int q0 = (int)(G * S0 + qj * PF / kQueues), q1 = (int)(G * S0 + (qj + 1) * PF / kQueues);
+    int nq = 0;
+    for (int g2 = qj; DYN && g2 * 8 < G; g2 += kQueues) nq += min(8, G - 8 * g2);
+    const int rank = 8 * (grp / kQueues) + (blk & 7);
+    const int b0 = DYN ? blk * S0 : (int)(blk * F / G), b1 = DYN ? (int)F : (int)((blk + 1) * F / G);
+    const int groups = DYN ? 0 : (b1 - b0 + P - 1) / P;  // rounds (block-uniform; static)
+    auto pool_item = [&](int gr) -> int {  // DYN, gr >= S0
+        const int j = gr - S0;
+        return j == 0 ? rank : j == 1 ? nq + rank : fs.rnd[gr & 3];
+    };
     auto live = [&](int gr) -> bool {
-        if constexpr (FUSED) return b0 + __builtin_amdgcn_readfirstlane(fs.rnd[gr & 3]) < b1;
+        if constexpr (DYN) return gr < S0 || q0 + __builtin_amdgcn_readfirstlane(pool_item(gr)) < q1;
         else return gr < groups;
     };
     auto round_base = [&](int gr) -> int {
-        if constexpr (FUSED) return b0 + fs.rnd[gr & 3];
+        if constexpr (DYN) return gr < S0 ? b0 + gr : q0 + pool_item(gr);
         else return b0 + gr * P;
     };
     if (!live(0)) return;
@@ -444,13 +461,13 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     auto consume = [&](int gr, auto slot_tag) __attribute__((always_inline)) {
         constexpr int RS = decltype(slot_tag)::value;
         int claimed = 0;
-        if constexpr (FUSED) {  // round gr + 2, claimed while this one streams (written to LDS before the barrier)
-            if (tid == 0) claimed = live(gr + 1) ? fs.claim_base + (int)claim_one(fs.queue) : kDeadClaim;
+        if constexpr (DYN) {  // pool round gr + 2 >= S0 + 2, claimed while this one streams (written to LDS before the barrier)
+            if (tid == 0 && gr >= S0) claimed = live(gr + 1) ? 2 * nq + (int)claim_one(fs.queue + qj * 32) : kDeadClaim;
         }
         uint2 sw[NW], mw[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) sw[w] = sw_n[RS][w], mw[w] = mw_n[RS][w];
-        if (FUSED || gr + kRing < groups) advance_issue();
+        if (DYN || gr + kRing < groups) advance_issue();
         issue_window(sw_n[RS], mw_n[RS]);
         float acc[NW][4] = {};
 #pragma unroll
@@ -473,7 +490,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
         }
 #pragma unroll
         for (int s = kPrefetch - kLag; s < kPrefetch; ++s) issue_slot(ring[RS], s);
-        if (!FUSED && gr >= groups) return;  // the phantom round
+        if (!DYN && gr >= groups) return;  // the phantom round
         const int item = round_base(gr) + ip;
         if constexpr (Q == 1) {
             if (item < b1) epilogue(item, acc[0], acc[1]);
@@ -483,8 +500,8 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
             for (int w = 0; w < NW; ++w)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) mine[w][v][lane] = acc[w][v];
-            if constexpr (FUSED) {
-                if (tid == 0) fs.rnd[(gr + 2) & 3] = claimed;
+            if constexpr (DYN) {
+                if (tid == 0 && gr >= S0) fs.rnd[(gr + 2) & 3] = claimed;
             }
             // every wave's partial tile of this round is in LDS (the loads in flight stay in flight); the next
             // write to this half of red comes after the next round's barrier, when these reads are done
@@ -501,8 +518,8 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
             }
         }
     };
-    if constexpr (FUSED) {
-        static_assert(!FUSED || (Q > 1 && kRing == 1), "the claims are published at the round's barrier");
+    if constexpr (DYN) {
+        static_assert(!DYN || (Q == 8 && kRing == 1), "one item a round; the claims are published at the round's barrier");
         // a live round always issues the next one's loads (clamped when that one is dead): one path for the ring
         int gr = 0;
         for (;; ++gr) {
@@ -522,12 +539,26 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave moves on
 }
 
-template <int NV, int Q>
+// The pool counters of a launch: sync's set epoch & 1, one 128-byte line a part (block 0 zeroes the other set, which
+// the next launch on this sync uses).
+__device__ FusedSched make_sched(LayerSync *sync, uint32_t epoch, int *s_rnd, const uint64_t *tagged, uint64_t *trace,
+                                 int *flag) {
+    if (blockIdx.x == 0 && threadIdx.x < kQueues)
+        __hip_atomic_store(&sync->queues[(epoch + 1) & 1][threadIdx.x][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return FusedSched{sync, &sync->queues[epoch & 1][0][0], s_rnd, tagged, epoch, trace, flag};
+}
+
+// DYN: the items after the fixed runs come from the pool of p.sync (Q = 8).
+template <int NV, int Q, bool DYN>
 __global__ void __launch_bounds__(kThreads) gate_up_kernel(GateUpParams p) {
     __shared__ __attribute__((aligned(16))) GuLds L;
     __shared__ Routes R;
     __shared__ __attribute__((aligned(16))) uint32_t emask[kMaxExperts];
-    gate_up_body<NV, Q, false>(p, L, R, emask, FusedSched{});
+    __shared__ int s_flag, s_rnd[4];
+    if constexpr (DYN)
+        gate_up_body<NV, Q, false, true>(p, L, R, emask, make_sched(p.sync, p.epoch, s_rnd, nullptr, nullptr, &s_flag));
+    else
+        gate_up_body<NV, Q, false, false>(p, L, R, emask, FusedSched{});
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -910,22 +941,7 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerParams lp) {
         if (trace && tid == 0) trace[i] = __builtin_amdgcn_s_memrealtime();
     };
     stamp(0);
-    // The first two gate_up rounds of every block are fixed: the nq blocks sharing queue j (groups of 8 consecutive
-    // blocks g = j, j + kQueues, ..., all full but the grid's last) take rounds r and nq + r, r = the block's rank
-    // among them; the queue's counter then numbers the rounds from 2 nq on. No atomic at the start of the launch
-    // (one would hold up every load issued after it until its turn on the contended counter came).
-    const int grp = b >> 3, qj = grp % kQueues;
-    int nq = 0;
-    for (int g2 = qj; g2 * 8 < G; g2 += kQueues) nq += min(8, G - 8 * g2);
-    uint32_t *queue = &sync->queues[lp.epoch & 1][qj][0];
-    const FusedSched fs{sync, queue, s_rnd, 2 * nq, lp.tagged, lp.epoch, trace, &s_flag};
-    if (tid == 0) {
-        const int r = 8 * (grp / kQueues) + (b & 7);
-        s_rnd[0] = r;
-        s_rnd[1] = nq + r;
-    }
-    if (b == 0 && tid < kQueues)  // the other set of counters, used by the next launch, starts from zero
-        __hip_atomic_store(&sync->queues[(lp.epoch + 1) & 1][tid][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const FusedSched fs = make_sched(sync, lp.epoch, s_rnd, lp.tagged, trace, &s_flag);
 
     // phase A: the router projection, rows [a R / PA, (a + 1) R / PA) for a = b, b + G, ... (at most kProjRows each)
     const int rows = lp.rows, PA = max(G, (rows + kProjRows - 1) / kProjRows);
@@ -954,7 +970,14 @@ hipError_t launch_gate_up(const GateUpParams &p, int cus, hipStream_t stream) {
     const int q = (int)(p.K / 512);  // K in {512, 1024, 2048, 4096}: four spans a wave
     const dim3 grid((unsigned)cus);
     auto go = [&](auto nv_tag, auto q_tag) {
-        gate_up_kernel<decltype(nv_tag)::value, decltype(q_tag)::value><<<grid, kThreads, 0, stream>>>(p);
+        constexpr int NV = decltype(nv_tag)::value, QQ = decltype(q_tag)::value;
+        if constexpr (QQ == 8) {
+            if (p.sync) {
+                gate_up_kernel<NV, QQ, true><<<grid, kThreads, 0, stream>>>(p);
+                return;
+            }
+        }
+        gate_up_kernel<NV, QQ, false><<<grid, kThreads, 0, stream>>>(p);
     };
     auto by_q = [&](auto nv_tag) {
         if (q == 1) go(nv_tag, std::integral_constant<int, 1>{});
@@ -1029,6 +1052,18 @@ int check_down(const char *fn, int64_t M, int64_t A, int64_t Ew, const sx_qview 
     return SX_OK;
 }
 
+std::atomic<uint64_t *> g_layer_trace{nullptr};
+
+// The launch number of a sync buffer: 1, 2, ... (never 0, the value of a freshly zeroed buffer).
+uint32_t next_epoch(const void *sync) {
+    static std::mutex mu;
+    static std::unordered_map<const void *, uint32_t> epochs;
+    std::lock_guard<std::mutex> lock(mu);
+    uint32_t &e = epochs[sync];
+    if (++e == 0) ++e;
+    return e;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1044,7 +1079,7 @@ int sx_moe_verify_supported(int64_t M, int64_t A, int64_t E, int64_t k, int64_t 
 int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
                           const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *w, int64_t Ew,
                           int32_t *ids, float *coef, void *h, float *h_sums, int act, uint32_t *router_err,
-                          uint32_t *expert_err, sx_stream stream) {
+                          uint32_t *expert_err, void *sync, sx_stream stream) {
     const char *fn = "sx_moe_verify_gate_up";
     const int64_t A = k + (shared_logit ? 1 : 0);
     SX_CHECK(x != nullptr && logits != nullptr && ids != nullptr && coef != nullptr && h != nullptr &&
@@ -1064,6 +1099,11 @@ int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t
     p.logits = logits, p.ld = ld, p.shared_logit = shared_logit, p.shared_ld = shared_ld, p.shared_id = shared_id;
     p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = w->N / Ew, p.K = w->K;
     p.ids = ids, p.coef = coef, p.h = static_cast<uint16_t *>(h), p.h_sums = h_sums, p.router_err = router_err, p.expert_err = expert_err;
+    if (sync != nullptr) {
+        SX_CHECK(aligned(sync, 16), fn, " sync must be 16-byte aligned");
+        p.sync = static_cast<vf::LayerSync *>(sync);
+        p.epoch = next_epoch(sync);
+    }
     SX_HIP(vf::launch_gate_up(p, device_cus(), stream_of(stream)), fn);
     return SX_OK;
 }
@@ -1083,20 +1123,6 @@ int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A,
     p.expert_err = expert_err;
     SX_HIP(vf::launch_down(p, stream_of(stream)), fn);
     return SX_OK;
-}
-
-namespace {
-std::atomic<uint64_t *> g_layer_trace{nullptr};
-
-// The launch number of a sync buffer: 1, 2, ... (never 0, the value of a freshly zeroed buffer).
-uint32_t next_epoch(const void *sync) {
-    static std::mutex mu;
-    static std::unordered_map<const void *, uint32_t> epochs;
-    std::lock_guard<std::mutex> lock(mu);
-    uint32_t &e = epochs[sync];
-    if (++e == 0) ++e;
-    return e;
-}
 }
 
 int sx_moe_verify_layer_trace(uint64_t *buf) {

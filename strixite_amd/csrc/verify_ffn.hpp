@@ -11,6 +11,8 @@ constexpr int kMaxSpansGu = 32;      // gate_up K <= 4096
 constexpr int kMaxSpansDn = 16;      // down K <= 2048
 constexpr int kHsElems = 64 * 1032;  // down: M * A * (K + 8) BF16 rows of h in LDS
 
+struct LayerSync;
+
 struct GateUpParams {
     const uint16_t *x;  // BF16 [M, K]
     int M, A, k, E, Ew;  // tokens, slots a token (k + shared), top-k, routed experts, experts in the weight
@@ -27,6 +29,8 @@ struct GateUpParams {
     uint16_t *h;        // BF16 [M * A, I]
     float *h_sums;      // nullable: FP32 [M * A, ceil(I / 16)], each 16-feature run of an h row summed as stored
     uint32_t *router_err, *expert_err;
+    LayerSync *sync;    // nullable: after a fixed run a block, items from the pool counter of its set epoch & 1
+    uint32_t epoch;
 };
 
 struct DownParams {
@@ -48,9 +52,9 @@ struct DownParams {
 // work counters alternate between two sets by epoch parity. Zero before the first launch; nothing to reset after one.
 constexpr int kMaxBlocks = 1024;
 constexpr int kMaxRouterRows = 1040;  // router weight rows: E + 1 <= 1025
-constexpr int kQueues = 16;           // gate_up work queues
+constexpr int kQueues = 16;           // counter lines a set (the gate_up pool uses the first)
 struct LayerSync {
-    uint32_t queues[2][kQueues][32];  // gate_up round counters, one 128-byte line each; set epoch & 1 in use (the
+    uint32_t queues[2][kQueues][32];  // gate_up pool counter ([set][0][0]), 128-byte lines; set epoch & 1 in use (the
                                       // other one is zeroed during the launch for the next)
     uint32_t done_b[kMaxBlocks];  // routing + gate_up + SwiGLU (h, h_sums) done
     uint64_t tagged[kMaxTokens * kMaxRouterRows];  // the router logits as (epoch << 32 | value bits) [M, rows]

@@ -132,9 +132,11 @@ def verify_supported(M, A, E, k, Ew, gate_up, down, act=ACT_BF16):
 
 
 def verify_gate_up(x, logits, w, E, k, Ew=None, shared_logit=None, shared_id=0, ids=None, coef=None, h=None,
-                   router_err=None, expert_err=None, h_sums=None, stream=None):
+                   router_err=None, expert_err=None, h_sums=None, sync=None, stream=None):
     """moe_router + gather_swiglu in one launch at verify width: ids, coef [M, A], h [M, A, I]. h_sums (optional,
-    FP32 [M * A, ceil(I / 16)]) receives the 16-feature sums of h that verify_down can take."""
+    FP32 [M * A, ceil(I / 16)]) receives the 16-feature sums of h that verify_down can take. sync (optional,
+    verify_layer_sync(), one per stream): after a fixed run each compute unit takes weight tiles from a shared pool
+    (K = 4096), so the faster ones take more; same outputs."""
     M, ld = x.shape[0], logits.stride(0)
     Ew = E if Ew is None else Ew
     A = k + (shared_logit is not None)
@@ -148,7 +150,7 @@ def verify_gate_up(x, logits, w, E, k, Ew=None, shared_logit=None, shared_id=0, 
     sld = 0 if shared_logit is None else shared_logit.stride(0)
     check(lib().sx_moe_verify_gate_up(_p(x), M, _p(logits), ld, E, k, _p(shared_logit), sld, shared_id, w.view(), Ew,
                                       _p(ids), _p(coef), _p(h), _p(h_sums), act_of(x), _p(router_err),
-                                      _p(expert_err), _s(stream)))
+                                      _p(expert_err), _p(sync), _s(stream)))
     return ids, coef, h, router_err, expert_err
 
 
@@ -165,7 +167,7 @@ def verify_down(h, w, ids, coef, Ew, y=None, expert_err=None, h_sums=None, strea
 
 
 def verify_layer_sync(device="cuda"):
-    """A zeroed sync buffer for verify_layer (one per stream; every launch leaves it zero)."""
+    """A zeroed sync buffer for verify_layer and verify_gate_up (one per stream; each launch readies it for the next)."""
     n = ctypes.c_size_t()
     check(lib().sx_moe_verify_layer_sync_bytes(ctypes.byref(n)))
     return torch.zeros((n.value + 3) // 4, dtype=torch.int32, device=device)

@@ -11,8 +11,8 @@ from . import kernels as kx
 class MoeVerifyLayer:
     """One MoE FFN sublayer. Weights: Wr FP32 [E, d], gate_up q4 [E * 2I, d], down q4 [E * d, I] (experts stacked,
     runtime/qwen4exp.cpp:126-129). At verify width (the shapes kernels.verify_supported takes) three launches:
-    router projection -> routing + gate_up + SwiGLU -> down + combine (the sequence qwen4exp.cpp:1139-1163 runs below
-    kGroupedMinTokens). Otherwise (or fused=False): router projection -> moe_router + moe_group_routes -> grouped
+    router projection -> routing + gate_up + SwiGLU (the tails of its compute units' shares balanced through a sync
+    buffer the layer owns) -> down + combine (the sequence qwen4exp.cpp:1139-1163 runs below kGroupedMinTokens). Otherwise (or fused=False): router projection -> moe_router + moe_group_routes -> grouped
     gate_up with the SwiGLU epilogue -> grouped down + combine."""
 
     def __init__(self, Wr, gate_up, down, E, k, max_tokens, act_dtype=torch.bfloat16, fused=True):
@@ -34,6 +34,7 @@ class MoeVerifyLayer:
         self.partial = torch.empty((M * A, self.d), dtype=torch.float32, device=dev)
         self.y = torch.empty((M, self.d), dtype=act_dtype, device=dev)
         self.fused = fused and act_dtype == torch.bfloat16
+        self.sync = kx.verify_layer_sync(dev) if self.fused else None  # one per stream: forwards run in stream order
 
     def _fused(self, M):
         return self.fused and kx.verify_supported(M, self.k, self.E, self.k, self.E, self.gate_up, self.down)
@@ -46,7 +47,7 @@ class MoeVerifyLayer:
         if self._fused(M):
             kx.verify_gate_up(x, self.logits[:M], self.gate_up, self.E, self.k, ids=self.ids[:M], coef=self.coef[:M],
                               h=self.h[:M], router_err=self.router_err, expert_err=self.expert_err,
-                              h_sums=self.h_sums, stream=stream)
+                              h_sums=self.h_sums, sync=self.sync, stream=stream)
             kx.verify_down(self.h[:M], self.down, self.ids[:M], self.coef[:M], self.E, y=self.y[:M],
                            expert_err=self.expert_err, h_sums=self.h_sums, stream=stream)
             return self.y[:M]

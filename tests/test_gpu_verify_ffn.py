@@ -151,3 +151,32 @@ def test_verify_supported_limits():
     logits = torch.zeros((2, 9), dtype=torch.float32, device="cuda")
     with pytest.raises(sx.SxError, match="shared_id"):  # a shared slot needs a valid expert row block
         kx().verify_gate_up(x, logits, gu, 8, 4, shared_logit=logits[:, 8:], shared_id=-1)
+
+
+@pytest.mark.parametrize("M,E,k,shared", [(6, 512, 10, False), (5, 64, 8, True), (1, 8, 1, False)])
+def test_verify_gate_up_pool_matches_static_split(M, E, k, shared):
+    """gate_up with a sync buffer (fixed runs, then the shared pool; K = 4096) gives the same ids, coef, h and
+    h_sums, bit for bit, as the fixed split, over launches back to back on one buffer (both counter sets in turn);
+    (1, 8, 1): fewer tiles than compute units, so no fixed run and most blocks get no round."""
+    import torch
+    from strixite_amd import synthetic as syn
+    d, I = 4096, 1024
+    Ew = E + (1 if shared else 0)
+    gu = syn.qweight(4, Ew * 2 * I, d, 128, seed=81)
+    sy = kx().verify_layer_sync()
+    A = k + (1 if shared else 0)
+    for r in range(5):
+        print(f"pool: M={M} E={E} k={k} shared={shared} launch {r}", flush=True)
+        x = syn.activations(M, d, seed=90 + r)
+        L = torch.randn((M, Ew), device="cuda") * 1.5
+        sl = L[:, E:] if shared else None
+        outs = []
+        for s in (None, sy):
+            hs = torch.full((M * A, I // 16), float("nan"), dtype=torch.float32, device="cuda")
+            ids, coef, h, rerr, eerr = kx().verify_gate_up(x, L, gu, E, k, Ew=Ew, shared_logit=sl, shared_id=E,
+                                                           h_sums=hs, sync=s)
+            sync()
+            assert list(rerr.cpu().numpy()[:3]) == [0, 0, 0] and list(eerr.cpu().numpy()[:3]) == [0, 0, 0]
+            outs.append((ids.cpu().numpy(), coef.cpu().numpy(), util.host_bits(h), hs.cpu().numpy()))
+        for a, b, name in zip(outs[0], outs[1], ("ids", "coef", "h", "h_sums")):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name} differs with the pool"
