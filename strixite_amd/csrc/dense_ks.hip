@@ -1,8 +1,8 @@
 // Dense dequantizing GEMV at decode / verify width (M <= 16 activation rows): y[M, N] = x[M, K] . deq(W)^T for q4
 // (G = 128 or 64) and q8 (G = 64), one or two quantization groups a 16-byte-a-lane span (kernels/linear_q4.hpp:26-30,
 // kernels/linear_q8.hpp:13-14), for the served shapes (4-64 spans a row) in place of qmm's dense mode (a wave a
-// 16-row tile over the whole K, many tiles a CU in flight at once). A block a CU takes an equal run of the 16-row
-// tiles (to within one tile), and its 8 waves split K Q ways (Q = min(8, spans / 4)) and work on 8 / Q tiles at a
+// 16-row tile over the whole K, many tiles a CU in flight at once). A block a CU takes an equal share of the 16-row
+// tiles (to within one tile; every G-th tile), and its 8 waves split K Q ways (Q = min(8, spans / 4)) and work on 8 / Q tiles at a
 // time, so every wave of the grid issues the same loads: SPW spans a round (4 or 8 loads of 1 KB), one round in
 // flight, and a CU reads one tile's rows at a time (measured faster than more tiles in flight a CU). The activation
 // rows sit in LDS once per block (BF16 x: one plane; FP32 x: three exact BF16 planes) in the B operand's code order
@@ -63,13 +63,19 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem);                       // [NPL][MP][K + 8]
     float *xsum = reinterpret_cast<float *>(smem + (size_t)NPL * MP * ldx * 2);  // [nspan * GS][16]
 
-    // this block's tiles [b0, b1), in rounds of P
+    // this block's tiles tile_of(j), j < ntile, in rounds of P: strided, blk + j G (the grid sweeps the rows
+    // together: the q8 LM head 122 -> 119 us), else the run b0 + j (fewer tiles a block: config 2 q8 16.2 against
+    // 17.3 us strided)
     const int64_t T16 = (N + 15) / 16;
-    const int b0 = (int)(blockIdx.x * T16 / gridDim.x), b1 = (int)((blockIdx.x + 1) * T16 / gridDim.x);
-    const int groups = (b1 - b0 + P - 1) / P;
+    const int G = (int)gridDim.x, blk = (int)blockIdx.x;
+    const bool strided = p.strided != 0;
+    const int b0 = (int)(blk * T16 / G);
+    const int ntile = strided ? (blk < T16 ? (int)((T16 - 1 - blk) / G + 1) : 0) : (int)((blk + 1) * T16 / G) - b0;
+    const int groups = (ntile + P - 1) / P;
+    auto tile_of = [&](int j) { return strided ? j * G + blk : b0 + j; };
 
-    // weight ring: round r = the slice kq of tile b0 + r P + ip (clamped into the run: a clamped round loads a
-    // valid tile and stores nothing); the round's scales / mins as one window of SPW BF16 a row
+    // weight ring: round r = the slice kq of tile tile_of(r P + ip) (clamped into the block's tiles: a clamped round
+    // loads a valid tile and stores nothing); the round's scales / mins as one window of SPW BF16 a row
     using Win = std::conditional_t<SPW * GS == 4, uint2, std::conditional_t<SPW * GS == 8, uint4, Win16>>;
     const int64_t rowbytes = K * BITS / 8, ngroups = (int64_t)nspan * GS;
     uint4 ring[kRingKs][SPW];
@@ -78,7 +84,7 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     const uint8_t *iq = p.q;
     const uint16_t *is_ = p.scale, *im = p.minv;
     auto iplace = [&]() {
-        const int tile = min(b0 + ii * P + ip, b1 - 1);
+        const int tile = tile_of(min(ii * P + ip, ntile - 1));
         const int64_t n = (int64_t)tile * 16 + n16, row = n < N ? n : N - 1;
         iq = p.q + row * rowbytes + (int64_t)kq * SPW * kSpanBytes + g * 16;
         is_ = p.scale + row * ngroups + kq * SPW * GS;
@@ -216,9 +222,9 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
 #pragma unroll
         for (int s = SPW - kLagKs<SPW>; s < SPW; ++s) issue_slot(ring[RS], s);
         if (gr >= groups) return;  // the phantom round
-        const int tile = b0 + gr * P + ip;
+        const int jt = gr * P + ip, tile = tile_of(jt);
         if (Q == 1) {
-            if (tile < b1)
+            if (jt < ntile)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) store(tile, v, acc[v]);
             return;
@@ -229,7 +235,7 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
         // every wave's partial tile of this round is in LDS (the loads in flight stay in flight); the next write to
         // this half of red comes after the next round's barrier, when these reads are done
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (tile < b1 && st_lane) {
+        if (jt < ntile && st_lane) {
             for (int j = 0; j < VS; ++j) {
                 float sum = 0.f;
                 for (int qq = 0; qq < Q; ++qq) sum += red[gr & 1][ip * Q + qq][vb + j][lane];  // K order
@@ -295,6 +301,7 @@ hipError_t launch(int bits, int64_t G, int act, int out_act, const Params &p0, i
     if (nspan >= 8 && tiles_per_block >= 2 * (kWaves / q8)) p.Q = (int)q8;
     else p.Q = (int)(nspan / 4 < kWaves ? nspan / 4 : kWaves);
     const int spw = (int)(nspan / p.Q);
+    p.strided = tiles_per_block >= 16 ? 1 : 0;
     const size_t lds = lds_bytes(act, p.M, p.K, bits, G);
     auto by_spw = [&](auto bits_tag, auto gs_tag, auto npl_tag, auto tx, auto ty) {
         constexpr int B = decltype(bits_tag)::value, GS = decltype(gs_tag)::value, NPL = decltype(npl_tag)::value;

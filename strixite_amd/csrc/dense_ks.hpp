@@ -13,14 +13,13 @@ struct Params {
     void *y;        // [M, N] (BF16 or FP32)
     int M;
     int Q;          // K slices a tile (set by launch)
+    int strided;    // a block's tiles: every G-th one (set by launch for 16 or more a block), else an adjacent run
     int64_t N, K;
 };
 
 size_t lds_bytes(int act, int64_t M, int64_t K, int bits, int64_t G);
 // q4 G = 128 or 64 or q8 G = 64, K of 4 .. 64 spans (a power of two), M <= 16, act / out_act as linear's (BF16 -> BF16 or
-// FP32, FP32 -> FP32), the activation planes within kLdsMax, and no more 16-row tiles than blocks (cus): with more,
-// qmm's dense mode already fills the chip and measured as fast or faster (configs 2 and 5: 11.7 vs 12.6 us, 81 vs
-// 84 us; config 1, 256 tiles: 14.4 vs 12.1 us)
+// FP32, FP32 -> FP32) and the activation planes within kLdsMax; any number of 16-row tiles
 bool eligible(int bits, int64_t G, int64_t N, int64_t K, int64_t M, int act, int out_act, int cus);
 hipError_t launch(int bits, int64_t G, int act, int out_act, const Params &p, int cus, hipStream_t stream);
 
