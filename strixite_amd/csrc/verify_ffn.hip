@@ -199,8 +199,9 @@ __device__ bool block_wait(const uint32_t *flags, int n, uint32_t epoch, uint32_
 //
 // FUSED (the one-launch layer): the logits come from the projection phase (agent-scope loads of the tagged pairs),
 // h and its sums are stored at agent scope for the down phase of every block.
-// DYN (the one-launch layer; gate_up with a sync buffer): a block streams a fixed run of S0 items first (S0 = about
-// 4/5 of an equal share: a run of adjacent tiles streams faster than tiles taken one by one), then items from the
+// DYN (the one-launch layer; gate_up with a sync buffer): a block streams S0 fixed items first (S0 = about 4/5 of an
+// equal share, every G-th item: the grid sweeps the weights together, which streams faster than tiles claimed one
+// by one and than a run of adjacent tiles a block), then items from the
 // pool after all the runs, one round at a time from its part of the pool (kQueues parts, each shared by blocks on
 // every XCD): its first two fixed, the rest claimed from the part's counter two rounds ahead. A block that streams
 // faster takes more of the pool, so the blocks finish within about a round of each other however unevenly the
@@ -324,7 +325,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     }
 
     // 3. the items of U x T16 (expert-major). Static: this block's run [b0, b1) in rounds of P. DYN: rounds of one
-    // item (Q = 8), rounds gr < S0 from the run [blk S0, blk S0 + S0), then items q0 + j of the block's part
+    // item (Q = 8), rounds gr < S0 the items gr G + blk (the grid sweeps the items together), then items q0 + j of the block's part
     // [q0, q1) of the pool [G S0, F): j = r and nq + r for the first two (r: the block's rank among the nq blocks of
     // the part), then the claims in fs.rnd[gr & 3], from 2 nq on
     const int T16 = (int)((Nrows + 15) / 16);
@@ -337,7 +338,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     int nq = 0;
     for (int g2 = qj; DYN && g2 * 8 < G; g2 += kQueues) nq += min(8, G - 8 * g2);
     const int rank = 8 * (grp / kQueues) + (blk & 7);
-    const int b0 = DYN ? blk * S0 : (int)(blk * F / G), b1 = DYN ? (int)F : (int)((blk + 1) * F / G);
+    const int b0 = DYN ? 0 : (int)(blk * F / G), b1 = DYN ? (int)F : (int)((blk + 1) * F / G);
     const int groups = DYN ? 0 : (b1 - b0 + P - 1) / P;  // rounds (block-uniform; static)
     auto pool_item = [&](int gr) -> int {  // DYN, gr >= S0
         const int j = gr - S0;
@@ -348,7 +349,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
         else return gr < groups;
     };
     auto round_base = [&](int gr) -> int {
-        if constexpr (DYN) return gr < S0 ? b0 + gr : q0 + pool_item(gr);
+        if constexpr (DYN) return gr < S0 ? gr * G + blk : q0 + pool_item(gr);
         else return b0 + gr * P;
     };
     if (!live(0)) return;
