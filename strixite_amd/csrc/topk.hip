@@ -103,7 +103,8 @@ __device__ __forceinline__ uint64_t wave_topk_sorted(const uint64_t (&key)[P], i
 }
 
 // wave_topk_sorted's result by ranks instead of sorts: the threshold T is the value word of the k-th best lane
-// maximum (a search two bits a step with ballots), so every top-k key has a value word >= T; the keys that reach it
+// maximum (a search two bits a step with ballots, over its top 16 bits: a T with its low bits cleared is still at
+// most that maximum, and admits only keys within 2^-7 of it besides), so every top-k key has a value word >= T; the keys that reach it
 // (a superset of the top k, ties at T included) go to the wave's LDS row by ballot positions, each takes its rank
 // among them from broadcast reads (keys are unique: ids differ), and the best k land at their ranks. More than 128
 // such keys (heavy ties at T) take the sorting path.
@@ -115,7 +116,7 @@ __device__ __forceinline__ uint64_t wave_topk(const uint64_t (&key)[P], int k, u
     for (int p = 0; p < P; ++p) head = umax(head, key[p]);
     const uint32_t hh = (uint32_t)(head >> 32);
     uint32_t T = 0u;
-    for (int b = 30; b >= 0; b -= 2) {  // uniform
+    for (int b = 30; b >= 16; b -= 2) {  // uniform
         const uint32_t t1 = T | (1u << b), t2 = T | (2u << b), t3 = T | (3u << b);
         const int c1 = __popcll(__ballot(hh >= t1)), c2 = __popcll(__ballot(hh >= t2)), c3 = __popcll(__ballot(hh >= t3));
         T = c3 >= k ? t3 : c2 >= k ? t2 : c1 >= k ? t1 : T;
@@ -202,6 +203,11 @@ __global__ void __launch_bounds__(kTopkThreads)
         for (int p = 0; p < kPer; ++p)
             if (g * kGroup + p * kTopkThreads + t >= n_in) key[p] = 0;
     }
+    // the last level of several: the first level's NaN flags of the row, loaded now (64 at a time across wave 0),
+    // used at the end
+    bool f1 = false;
+    if (!kLogits && groups == 1 && wave == 0)
+        for (int c = lane; c < groups1; c += 64) f1 |= nan_level1[r * groups1 + c] != 0u;
     __syncthreads();
     if (my_nan) atomicOr(&s_nan, 1u);
     const uint64_t mine = wave_topk<kPer>(key, k, scratch[wave], kScratch);
@@ -216,10 +222,17 @@ __global__ void __launch_bounds__(kTopkThreads)
     }
     if (groups > 1) {
         if (lane < k) out_keys[(r * groups + g) * k + lane] = best;
-    } else if (lane < k) {  // the last level: candidates with their values read back from the row (keeps -0)
+    } else if (lane < k) {  // the last level: candidates with their values from the keys (a zero read back from the
+                            // row: the key folds -0 onto +0)
         sx_logit_cand c;
-        if (best == 0) c.v = -INFINITY, c.id = INT32_MAX;
-        else c.id = key_id(best), c.v = logits[r * ld + c.id];
+        if (best == 0) {
+            c.v = -INFINITY, c.id = INT32_MAX;
+        } else {
+            const uint32_t hi = (uint32_t)(best >> 32);
+            c.id = key_id(best);
+            c.v = __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
+            if (c.v == 0.f) c.v = logits[r * ld + c.id];
+        }
         out_final[r * k + lane] = c;
     }
     if constexpr (kLogits) {
@@ -227,10 +240,8 @@ __global__ void __launch_bounds__(kTopkThreads)
             nan_level1[r * groups + g] = s_nan;
             if (groups == 1) nan[r] = s_nan;
         }
-    } else if (groups == 1) {  // the first level's flags of the row, 64 at a time across the wave
-        bool f = false;
-        for (int c = lane; c < groups1; c += 64) f |= nan_level1[r * groups1 + c] != 0u;
-        const bool any = __ballot(f) != 0;  // the whole wave votes
+    } else if (groups == 1) {  // the first level's flags of the row
+        const bool any = __ballot(f1) != 0;  // the whole wave votes
         if (lane == 0) nan[r] = any ? 1u : 0u;
     }
 }
