@@ -351,12 +351,14 @@ __global__ void __launch_bounds__(kPickThreads)
 // Lane 0 walks the rows in order, exactly as the engine's loop and the sampler's draw do on the host: the sums are
 // sequential in double, the draw r = u * kept with u the host's generate_canonical<double, 53> for that row. The
 // wave loads a row's candidates into LDS and computes their probabilities exp(v_i / T - v_0 / T) a lane each (the
-// same double arithmetic, once each) before lane 0's sequential walk reads them.
+// same double arithmetic, once each) before lane 0's sequential walk reads them; once lane 0 has their sum, the
+// quotients p_i / sum the top-p walk adds are taken a lane each too (each quotient is the same division whoever
+// makes it, so the walk's sums are unchanged).
 __global__ void __launch_bounds__(64)
     mtp_accept_kernel(const sx_logit_cand *cands, const uint32_t *nan, int kc, const int32_t *drafts, int k,
                       const double *u, double temperature, int top_k, double top_p, int64_t n_valid, int32_t *out) {
     __shared__ sx_logit_cand cs[64];
-    __shared__ double probs[64];
+    __shared__ double probs[64], quot[64], s_sum;
     __shared__ int s_go;
     const int lane = threadIdx.x;
     const int kk = (int)(top_k < n_valid ? top_k : n_valid);
@@ -364,9 +366,19 @@ __global__ void __launch_bounds__(64)
     for (;; ++j) {
         if (lane < kc) cs[lane] = cands[(int64_t)j * kc + lane];
         __syncthreads();
-        if (temperature != 0 && lane < kk && isfinite(cs[0].v))
-            probs[lane] = exp((double)cs[lane].v / temperature - (double)cs[0].v / temperature);
+        const bool sampled = temperature != 0 && isfinite(cs[0].v);  // uniform
+        if (sampled && lane < kk) probs[lane] = exp((double)cs[lane].v / temperature - (double)cs[0].v / temperature);
         __syncthreads();
+        if (sampled && top_p < 1) {
+            if (lane == 0) {
+                double sum = 0;
+                for (int i = 0; i < kk; ++i) sum += probs[i];
+                s_sum = sum;
+            }
+            __syncthreads();
+            if (lane < kk) quot[lane] = probs[lane] / s_sum;
+            __syncthreads();
+        }
         if (lane == 0) {
             const sx_logit_cand *c = cs;
             int32_t v = -1;
@@ -391,7 +403,7 @@ __global__ void __launch_bounds__(64)
                     if (top_p < 1) {
                         double acc = 0;
                         for (int i = 0; i < kk; ++i) {
-                            acc += probs[i] / sum;
+                            acc += quot[i];
                             if (acc >= top_p) {
                                 keep = i + 1;
                                 break;
