@@ -136,7 +136,6 @@ __device__ __forceinline__ uint4 load16_agent(const void *base, uint32_t bytes, 
 // The gate_up pool of a block: blocks 8j .. 8j + 7 (one on each XCD under the round-robin dispatch) share part
 // j mod kQueues, so every part is served by the same mix of XCDs and the parts drain together.
 __device__ __forceinline__ int queue_of(int block) { return (block >> 3) % kQueues; }
-constexpr int kDeadClaim = 1 << 24;  // a claim past the pool (the block's work is done)
 // The share of the gate_up items taken in fixed runs (the rest from the shared pool): kFixedNum / kFixedDen.
 constexpr int kFixedNum = 4, kFixedDen = 5;
 
@@ -461,9 +460,13 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     // 6. consume: A rows = tokens (lane row n16), D rows 4g .. 4g + 3 = tokens, columns = the 16 features
     auto consume = [&](int gr, auto slot_tag) __attribute__((always_inline)) {
         constexpr int RS = decltype(slot_tag)::value;
-        int claimed = 0;
-        if constexpr (DYN) {  // pool round gr + 2 >= S0 + 2, claimed while this one streams (written to LDS before the barrier)
-            if (tid == 0 && gr >= S0) claimed = live(gr + 1) ? 2 * nq + (int)claim_one(fs.queue + qj * 32) : kDeadClaim;
+        // DYN: pool round gr + 2 >= S0 + 2, claimed while this one streams and published before the round's barrier.
+        // Claimed whether or not the pool has run dry (a claim past the part's end is dead like every later one), and
+        // the claim's value used only where it is published: a select on it here would wait for the atomic's return
+        // (and every load issued before it) at once, holding the whole block up for a round trip to the counter.
+        uint32_t claim_raw = 0u;
+        if constexpr (DYN) {
+            if (tid == 0 && gr >= S0) claim_raw = claim_one(fs.queue + qj * 32);
         }
         uint2 sw[NW], mw[NW];
 #pragma unroll
@@ -502,7 +505,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
 #pragma unroll
                 for (int v = 0; v < 4; ++v) mine[w][v][lane] = acc[w][v];
             if constexpr (DYN) {
-                if (tid == 0 && gr >= S0) fs.rnd[(gr + 2) & 3] = claimed;
+                if (tid == 0 && gr >= S0) fs.rnd[(gr + 2) & 3] = 2 * nq + (int)claim_raw;
             }
             // every wave's partial tile of this round is in LDS (the loads in flight stay in flight); the next
             // write to this half of red comes after the next round's barrier, when these reads are done
