@@ -363,7 +363,11 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     const uint8_t *iq = p.q;
     const uint16_t *is_ = p.scale, *im = p.minv;
     auto iplace = [&]() {
-        const int item = min(round_base(ii) + ip, b1 - 1);
+        int item = round_base(ii) + ip;
+        if constexpr (DYN) {  // a dead pool round (past the part; usually still inside F) loads the round before's item
+            if (ii > 0 && ii >= S0 && item >= q1) item = round_base(ii - 1);  // again: an L2 hit, not an unused tile
+        }
+        item = min(item, b1 - 1);
         const int u = item / T16, tile = item - u * T16;
         const int64_t n = (int64_t)tile * 16 + n16, nn = n < Nrows ? n : Nrows - 1;
         const int64_t row = (int64_t)R.u_exp[u] * p.N + nn;
