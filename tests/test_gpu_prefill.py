@@ -44,6 +44,15 @@ def test_config4_prefill_layer_full_size():
     h = kx().gather_grouped(x, gu, E, ws, M, k, swiglu=True)
     y = kx().combine_grouped(h, dn, E, ids, coef, ws)
     sync()
+    # the grouped kernels order their loads and waits by hand: a second run must give the same bits (a wait that
+    # lets a load land after its use shows up as run-to-run differences long before it breaks a tolerance)
+    print("config 4: the grouped kernels again (run-to-run identical)", flush=True)
+    h2 = kx().gather_grouped(x, gu, E, ws, M, k, swiglu=True)
+    y2 = kx().combine_grouped(h, dn, E, ids, coef, ws)
+    sync()
+    assert torch.equal(h.view(torch.int16), h2.view(torch.int16)), "grouped gate_up differs between two runs"
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), "grouped down + combine differs between two runs"
+    del h2, y2
 
     xh = util.host_bits(x)
     util.assert_close(raw.cpu().numpy(), orc.linear_f32w(xh, Wr.cpu().numpy()), tol=1e-5, what="router logits")
