@@ -216,6 +216,21 @@ typedef struct sx_mtp_pick_s {
 } sx_mtp_pick_t;
 int sx_mtp_pick(const float *logits, int64_t n, const uint32_t *router_err, const uint32_t *expert_err,
                 const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out, sx_stream stream);
+/* The same pick (kernels/mtp_pick.hpp:20-33, the same output bit for bit) read by many blocks at once, one launch:
+ * each block reduces its run of the logits to a top-2 in `workspace` and the last block to finish merges them.
+ * workspace: device, 16-byte aligned, sx_mtp_pick_ws_bytes long, ZEROED before its first use (it holds a counter that
+ * every call leaves ready for the next). Calls that share a workspace must be ordered on one stream. */
+int sx_mtp_pick_ws_bytes(int64_t n, size_t *bytes);
+/* The MTP draft head's LM head and pick in one launch (runtime/qwen4exp.cpp:1408-1413: the head's logits, then
+ * kernels::mtp_pick over them): logits[N] = x[1, K] (BF16) . deq(w)^T in FP32 as sx_linear_q4 / q8 write them, and
+ * `out` the pick of those logits, bit-identical to sx_mtp_pick's. bits 4 or 8; workspace as sx_mtp_pick_ws's (zeroed
+ * before its first use). Shapes the fused GEMV does not take run sx_linear_q4 / q8 and then sx_mtp_pick_ws. */
+int sx_mtp_head_pick(const void *x, const sx_qview *w, int bits, float *logits, const uint32_t *router_err,
+                     const uint32_t *expert_err, const uint32_t *attn_err, const unsigned long long *emb_err,
+                     sx_mtp_pick_t *out, void *workspace, size_t workspace_bytes, sx_stream stream);
+int sx_mtp_pick_ws(const float *logits, int64_t n, const uint32_t *router_err, const uint32_t *expert_err,
+                   const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out, void *workspace,
+                   size_t workspace_bytes, sx_stream stream);
 
 /* ---- draft acceptance on the device: serve/engine.cpp:592-610 with Sampler semantics (serve/sampler.cpp:183-248) ----
  * cands [k+1, kc] (from sx_logits_topk, value desc), nan [k+1], drafts [k] (device). Row j is sampled (greedy:

@@ -96,6 +96,9 @@ SIGNATURES = {
     "sx_logits_topk_noalloc": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P],
     "sx_quantize_q4_from_q8": [_QV, _I64, _P, _P, _P, _P, _P],
     "sx_mtp_pick": [_P, _I64, _P, _P, _P, _P, _P, _P],
+    "sx_mtp_pick_ws_bytes": [_I64, _P],
+    "sx_mtp_head_pick": [_P, _QV, _INT, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P],
+    "sx_mtp_pick_ws": [_P, _I64, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P],
     "sx_mtp_accept": [_P, _P, _I64, _P, _I64, _P, _D, _I64, _D, _I64, _P, _P],
     "sx_strix_hash64": [_P, _U64],
     "sx_strixw_open": [_CP, ctypes.POINTER(_P)],

@@ -139,6 +139,33 @@ int sx_linear_q8(const void *x, const sx_qview *w, void *y, int64_t M, int act, 
     return linear("sx_linear_q8", 8, x, w, y, M, act, out_act, stream);
 }
 
+int sx_mtp_head_pick(const void *x, const sx_qview *w, int bits, float *logits, const uint32_t *router_err,
+                     const uint32_t *expert_err, const uint32_t *attn_err, const unsigned long long *emb_err,
+                     sx_mtp_pick_t *out, void *workspace, size_t workspace_bytes, sx_stream stream) {
+    const char *fn = "sx_mtp_head_pick";
+    SX_CHECK(bits == 4 || bits == 8, fn, " bits = ", bits, ", expected 4 or 8");
+    SX_CHECK(x && logits && router_err && expert_err && attn_err && emb_err && out && workspace, fn, " null pointer");
+    if (int rc = check_view(fn, w, bits)) return rc;
+    SX_CHECK(aligned(x, 16), fn, " x ", x, " must be 16-byte aligned for vector loads");
+    SX_CHECK(apart(x, w->K * 2, logits, w->N * 4), fn, " logits overlap x");
+    SX_CHECK(workspace_bytes >= sizeof(pick::Workspace), fn, " workspace ", workspace_bytes, " bytes, need ",
+             sizeof(pick::Workspace));
+    SX_CHECK(aligned(workspace, 16), fn, " workspace must be 16-byte aligned");
+    const pick::Args pa{static_cast<pick::Workspace *>(workspace), router_err, expert_err, attn_err, emb_err, out};
+    const int cus = device_cus();
+    if (cus <= pick::kMaxParts && dks::eligible(bits, w->G, w->N, w->K, 1, SX_ACT_BF16, SX_ACT_F32, cus)) {
+        dks::Params d{};
+        d.x = x, d.q = w->q, d.scale = w->scale, d.minv = w->minv, d.y = logits, d.M = 1, d.N = w->N, d.K = w->K;
+        d.pick = pa;
+        SX_HIP(dks::launch(bits, w->G, SX_ACT_BF16, SX_ACT_F32, d, cus, stream_of(stream)), fn);
+        return SX_OK;
+    }
+    // other shapes: the GEMV, then the pick over the logits
+    if (int rc = linear(fn, bits, x, w, logits, 1, SX_ACT_BF16, SX_ACT_F32, stream)) return rc;
+    return sx_mtp_pick_ws(logits, w->N, router_err, expert_err, attn_err, emb_err, out, workspace, workspace_bytes,
+                          stream);
+}
+
 int sx_linear_q4_experts_gather(const void *x, const sx_qview *w, int64_t E, const int32_t *ids, int64_t M, int64_t A,
                                 void *y, int act, uint32_t *err, sx_stream stream) {
     const char *fn = "sx_linear_q4_experts_gather";

@@ -14,6 +14,9 @@
 // q4 G = 64 (the MTP draft head) has two groups a span: a span's lanes 0-31 hold the first group's codes and lanes
 // 32-63 the second's, so each MFMA runs twice, once with the other group's lanes reading the zero row instead of the
 // activations (no ALU selects), and each group folds with its own scale, min and x sums.
+// PICK (the MTP draft head, FP32 logits, M = 1): each thread keeps the running top-2 of the logits it stores (its
+// indices ascend: its tiles do), and the blocks merge them at the end as pick::block_pick does, so the pick needs no
+// launch and no second read of the logits of its own.
 #include "dense_ks.hpp"
 #include "qmm_impl.hpp"
 
@@ -45,9 +48,16 @@ __device__ __forceinline__ float win_value(uint32_t dw, int s) {
     return __uint_as_float((s & 1) ? (dw & 0xFFFF0000u) : (dw << 16));
 }
 
-template <int BITS, int NPL, int SPW, int GS, typename TX, typename TY>
+template <int BITS, int NPL, int SPW, int GS, typename TX, typename TY, bool PICK>
 __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     static_assert(GS == 1 || (GS == 2 && BITS == 4), "two groups a span: q4 G = 64");
+    static_assert(!PICK || std::is_same_v<TY, float>, "the pick takes FP32 logits");
+    __shared__ pick::Top2 pick_red[PICK ? kWaves : 1];
+    __shared__ int pick_last;
+    pick::Top2 pk = pick::top2_none();
+    pick::ErrWords pk_errs{};
+    if constexpr (PICK)
+        pk_errs = pick::read_errs(threadIdx.x, p.pick.router_err, p.pick.expert_err, p.pick.attn_err, p.pick.emb_err);
     using F = qmm::detail::Fmt<BITS>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     __shared__ __attribute__((aligned(16))) float red[2][kWaves][4][64];  // [round & 1][wave][v][lane]
@@ -157,7 +167,10 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
         *reinterpret_cast<uint4 *>(xs + ((int64_t)(i / (ldx / 8)) * MP + M) * ldx + (int64_t)(i % (ldx / 8)) * 8) =
             uint4{0u, 0u, 0u, 0u};
     __syncthreads();
-    if (groups <= 0) return;
+    if (groups <= 0) {
+        if constexpr (PICK) pick::block_pick<kWaves>(pk, p.pick, pk_errs, pick_red, &pick_last);
+        return;
+    }
 
     // 2. consume: A rows = activation rows (lane row n16, zeros past M), D rows 4g .. 4g + 3, columns = the tile's rows
     const bool a_on = n16 < M;
@@ -175,7 +188,11 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     auto store = [&](int tile, int v, float val) __attribute__((always_inline)) {
         const int r = 4 * g + v;
         const int64_t n = (int64_t)tile * 16 + n16;
-        if (r < M && n < N) store_act(static_cast<TY *>(p.y), (int64_t)r * N + n, val);
+        if (r < M && n < N) {
+            store_act(static_cast<TY *>(p.y), (int64_t)r * N + n, val);
+            if constexpr (PICK)
+                if (r == 0) pick::top2_take(pk, val, n);
+        }
     };
     auto consume = [&](int gr, auto slot_tag) __attribute__((always_inline)) {
         constexpr int RS = decltype(slot_tag)::value;
@@ -251,11 +268,12 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
             (consume(gr + RS, std::integral_constant<int, RS>{}), ...);
         }(std::make_integer_sequence<int, kRingKs>{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the phantom round's loads land before the wave exits
+    if constexpr (PICK) pick::block_pick<kWaves>(pk, p.pick, pk_errs, pick_red, &pick_last);
 }
 
-template <int BITS, int NPL, int SPW, int GS, typename TX, typename TY>
+template <int BITS, int NPL, int SPW, int GS, typename TX, typename TY, bool PICK = false>
 hipError_t go(const Params &p, int cus, size_t lds, hipStream_t stream) {
-    auto fn = dense_ks_kernel<BITS, NPL, SPW, GS, TX, TY>;
+    auto fn = dense_ks_kernel<BITS, NPL, SPW, GS, TX, TY, PICK>;
     // the dynamic LDS limit, set once an instantiation (every launch asks for <= kLdsMax; setting it twice from two
     // threads is harmless)
     static std::atomic<bool> sized{false};
@@ -307,6 +325,15 @@ hipError_t launch(int bits, int64_t G, int act, int out_act, const Params &p0, i
         constexpr int B = decltype(bits_tag)::value, GS = decltype(gs_tag)::value, NPL = decltype(npl_tag)::value;
         using TX = decltype(tx);
         using TY = decltype(ty);
+        if (p.pick.ws != nullptr) {
+            if constexpr (std::is_same_v<TY, float> && NPL == 1) {
+                if (p.M != 1 || cus > pick::kMaxParts) return hipErrorInvalidValue;
+                return spw == 4 ? go<B, NPL, 4, GS, TX, TY, true>(p, cus, lds, stream)
+                                : go<B, NPL, 8, GS, TX, TY, true>(p, cus, lds, stream);
+            } else {
+                return hipErrorInvalidValue;  // the pick: BF16 x, FP32 logits
+            }
+        }
         return spw == 4 ? go<B, NPL, 4, GS, TX, TY>(p, cus, lds, stream) : go<B, NPL, 8, GS, TX, TY>(p, cus, lds, stream);
     };
     auto by_act = [&](auto bits_tag, auto gs_tag) {

@@ -1,6 +1,7 @@
 // Dense dequantizing GEMV at decode / verify width with K split over a block's waves (dense_ks.hip).
 #pragma once
 #include "common.hpp"
+#include "pick.hpp"
 
 namespace sx::dks {
 
@@ -15,6 +16,7 @@ struct Params {
     int Q;          // K slices a tile (set by launch)
     int strided;    // a block's tiles: every G-th one (set by launch for 16 or more a block), else an adjacent run
     int64_t N, K;
+    pick::Args pick;  // pick.ws set: the MTP pick of row 0 of y (FP32 y, M = 1) fused after the GEMV, gridDim <= 256
 };
 
 size_t lds_bytes(int act, int64_t M, int64_t K, int bits, int64_t G);

@@ -1,6 +1,7 @@
 // The verify tail on gfx950: logits top-k (kernels/logits_topk.hpp:3-46), the MTP draft pick (kernels/mtp_pick.hpp:3-33)
 // and draft acceptance on the device (serve/engine.cpp:592-610 with serve/sampler.cpp:183-248's draw).
 #include "common.hpp"
+#include "pick.hpp"
 
 #include <climits>
 #include <mutex>
@@ -251,35 +252,10 @@ int64_t groups_of(int64_t n) { return (n + kGroup - 1) / kGroup; }
 // ---------------- MTP draft pick ----------------
 constexpr int kPickThreads = 1024;
 
-struct Top2 {
-    float b1, b2;
-    int i1;  // INT_MAX: nothing seen
-    uint32_t nan;
-};
-
-__device__ __forceinline__ Top2 top2_merge(const Top2 &a, const Top2 &b) {
-    if (b.i1 == INT_MAX) return {a.b1, a.b2, a.i1, a.nan | b.nan};
-    if (a.i1 == INT_MAX) return {b.b1, b.b2, b.i1, a.nan | b.nan};
-    const bool a_wins = a.b1 > b.b1 || (a.b1 == b.b1 && a.i1 < b.i1);
-    const Top2 &w = a_wins ? a : b, &l = a_wins ? b : a;
-    return {w.b1, fmaxf(w.b2, l.b1), w.i1, a.nan | b.nan};  // the loser's best is at least its own runner-up
-}
-
-__device__ __forceinline__ Top2 top2_xor(const Top2 &p, int off) {
-    return {__shfl_xor(p.b1, off), __shfl_xor(p.b2, off), __shfl_xor(p.i1, off),
-            (uint32_t)__shfl_xor((int)p.nan, off)};
-}
-
-// One value into a thread's running top-2 (indices offered in ascending order: the strict > keeps the lower index of
-// equal values).
-__device__ __forceinline__ void top2_take(Top2 &p, float v, int64_t i) {
-    if (v != v) {
-        p.nan = 1u;
-        return;
-    }
-    if (p.i1 == INT_MAX || v > p.b1) p.b2 = p.b1, p.b1 = v, p.i1 = (int)i;
-    else if (v > p.b2) p.b2 = v;
-}
+using pick::top2_merge;
+using pick::top2_take;
+using pick::top2_xor;
+using pick::Top2;
 
 // VEC: 16-byte loads (n % 4 == 0, x 16-byte aligned), thread t taking elements 4j .. 4j + 3 for j = t, t + 1024, ...
 // Either way a thread's indices ascend, and its loads go out in batches of kPickBatch before any is used (the index
@@ -334,17 +310,62 @@ __global__ void __launch_bounds__(kPickThreads)
     p = lane < kPickThreads / 64 ? part[lane] : Top2{-INFINITY, -INFINITY, INT_MAX, 0u};
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) p = top2_merge(p, top2_xor(p, off));
-    if (lane == 0) {
-        out->best = p.i1 == INT_MAX ? 0 : p.i1;  // every logit NaN: 0, flagged
-        out->best_v = p.b1, out->second_v = p.b2, out->nan = p.nan;
-        out->pad = 0;
-        out->emb = *emb_err;
+    pick::write_pick(p, lane, pick::read_errs(lane, router_err, expert_err, attn_err, emb_err), out);
+}
+
+// The pick over many blocks (sx_mtp_pick_ws), one launch: block b reduces its run of the logits (its threads offer
+// their indices in ascending order, as mtp_pick_kernel's do) and the block that finishes last merges the blocks'
+// partials into the output (pick::block_pick); the merge does not depend on the split, so the output equals
+// mtp_pick_kernel's bit for bit. A single block reads the whole row through one compute unit (the served 65,536
+// logits: 12 us); 64 blocks read it at once.
+constexpr int kPickWsBlocks = 64, kPickWsThreads = 256;
+
+template <bool VEC>
+__global__ void __launch_bounds__(kPickWsThreads) mtp_pick_ws_kernel(const float *x, int64_t n, pick::Args a) {
+    __shared__ Top2 red[kPickWsThreads / 64];
+    __shared__ int last;
+    const int tid = threadIdx.x;
+    Top2 p = pick::top2_none();
+    const pick::ErrWords errs = pick::read_errs(tid, a.router_err, a.expert_err, a.attn_err, a.emb_err);
+    // the block's run [lo, hi): whole float4s when VEC
+    const int64_t per = VEC ? ((n / 4 + gridDim.x - 1) / gridDim.x) * 4 : (n + gridDim.x - 1) / gridDim.x;
+    const int64_t lo = (int64_t)blockIdx.x * per, hi = lo + per < n ? lo + per : n;
+    constexpr int kBatch = 4;
+    if constexpr (VEC) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        const int64_t a4 = lo / 4, b4 = hi / 4;
+        for (int64_t base = a4 + tid; base < b4; base += (int64_t)kBatch * kPickWsThreads) {
+            float4 v[kBatch];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int64_t j = base + (int64_t)b * kPickWsThreads;
+                v[b] = x4[j < b4 ? j : b4 - 1];
+            }
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int64_t j = base + (int64_t)b * kPickWsThreads;
+                if (j >= b4) break;
+                top2_take(p, v[b].x, 4 * j), top2_take(p, v[b].y, 4 * j + 1);
+                top2_take(p, v[b].z, 4 * j + 2), top2_take(p, v[b].w, 4 * j + 3);
+            }
+        }
+    } else {
+        for (int64_t base = lo + tid; base < hi; base += (int64_t)kBatch * kPickWsThreads) {
+            float v[kBatch];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int64_t i = base + (int64_t)b * kPickWsThreads;
+                v[b] = x[i < hi ? i : hi - 1];
+            }
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int64_t i = base + (int64_t)b * kPickWsThreads;
+                if (i >= hi) break;
+                top2_take(p, v[b], i);
+            }
+        }
     }
-    if (lane < 3) {
-        out->err[lane] = router_err[lane];
-        out->err[3 + lane] = expert_err[lane];
-        out->err[6 + lane] = attn_err[lane];
-    }
+    pick::block_pick<kPickWsThreads / 64>(p, a, errs, red, &last);
 }
 
 // ---------------- draft acceptance ----------------
@@ -552,6 +573,31 @@ int sx_mtp_pick(const float *logits, int64_t n, const uint32_t *router_err, cons
         mtp_pick_kernel<false><<<1, kPickThreads, 0, stream_of(stream)>>>(logits, n, router_err, expert_err, attn_err,
                                                                          emb_err, out);
     SX_LAUNCHED("mtp_pick n=", n);
+    return SX_OK;
+}
+
+int sx_mtp_pick_ws_bytes(int64_t n, size_t *bytes) {
+    SX_CHECK(bytes != nullptr, "null output");
+    SX_CHECK(n >= 1 && n <= INT_MAX, "n = ", n, " logits, expected 1..", INT_MAX);
+    *bytes = sizeof(pick::Workspace);
+    return SX_OK;
+}
+
+int sx_mtp_pick_ws(const float *logits, int64_t n, const uint32_t *router_err, const uint32_t *expert_err,
+                   const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out, void *workspace,
+                   size_t workspace_bytes, sx_stream stream) {
+    SX_CHECK(logits && router_err && expert_err && attn_err && emb_err && out && workspace, "null pointer");
+    SX_CHECK(n >= 1 && n <= INT_MAX, "n = ", n, " logits, expected 1..", INT_MAX);
+    SX_CHECK(workspace_bytes >= sizeof(pick::Workspace), "workspace ", workspace_bytes, " bytes, need ",
+             sizeof(pick::Workspace));
+    SX_CHECK(aligned(workspace, 16), "workspace must be 16-byte aligned");
+    hipStream_t s = stream_of(stream);
+    const pick::Args a{static_cast<pick::Workspace *>(workspace), router_err, expert_err, attn_err, emb_err, out};
+    if (n % 4 == 0 && aligned(logits, 16))
+        mtp_pick_ws_kernel<true><<<kPickWsBlocks, kPickWsThreads, 0, s>>>(logits, n, a);
+    else
+        mtp_pick_ws_kernel<false><<<kPickWsBlocks, kPickWsThreads, 0, s>>>(logits, n, a);
+    SX_LAUNCHED("mtp_pick_ws n=", n);
     return SX_OK;
 }
 

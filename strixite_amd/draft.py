@@ -12,7 +12,6 @@ draft is kept and chained, and which part of the verify the session keeps once t
 """
 import torch
 
-from . import ACT_F32, MtpPick
 from . import kernels as kx
 
 
@@ -26,16 +25,17 @@ class DraftHead:
         dev = lm_head_q8.q.device
         self.logits = torch.empty((1, mtp_vocab), dtype=torch.float32, device=dev)
         self.pick = torch.empty(64, dtype=torch.uint8, device=dev)
+        self.pick_ws = torch.zeros(kx.mtp_pick_ws_bytes(mtp_vocab), dtype=torch.uint8, device=dev)
         self.zero_err = torch.zeros(4, dtype=torch.int32, device=dev)
         self.zero_emb = torch.zeros(1, dtype=torch.int64, device=dev)
 
     def forward(self, h, router_err=None, expert_err=None, attn_err=None, emb_err=None, stream=None):
         """h: BF16 [1, d], the head's hidden state. Queues the logits and the pick (no synchronisation)."""
-        kx.linear(h, self.w, out_act=ACT_F32, y=self.logits, stream=stream)
         z = self.zero_err
-        return kx.mtp_pick(self.logits[0], router_err if router_err is not None else z,
-                           expert_err if expert_err is not None else z, attn_err if attn_err is not None else z,
-                           emb_err if emb_err is not None else self.zero_emb, out=self.pick, stream=stream)
+        return kx.mtp_head_pick(h, self.w, self.logits, router_err if router_err is not None else z,
+                                expert_err if expert_err is not None else z, attn_err if attn_err is not None else z,
+                                emb_err if emb_err is not None else self.zero_emb, self.pick_ws, out=self.pick,
+                                stream=stream)
 
     def top2(self):
         """The pick read back (one synchronisation, as forward_mtp_top2 does): an MtpPick."""

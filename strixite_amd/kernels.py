@@ -317,10 +317,32 @@ def quantize_q4_from_q8(w8, G=64, rows=None, err=None, stream=None):
     return QWeight(4, q, s, m, rows, w8.K, G), err
 
 
-def mtp_pick(logits, router_err, expert_err, attn_err, emb_err, out=None, stream=None):
+def mtp_pick_ws_bytes(n):
+    b = ctypes.c_size_t()
+    check(lib().sx_mtp_pick_ws_bytes(n, ctypes.byref(b)))
+    return b.value
+
+
+def mtp_pick(logits, router_err, expert_err, attn_err, emb_err, out=None, ws=None, stream=None):
+    """The 64-byte pick of `logits`. With `ws` (a zeroed device uint8 buffer of mtp_pick_ws_bytes, reused across
+    calls on one stream) the one-launch many-block pick runs; its output is bit-identical to the single-block one's."""
     out = torch.empty(64, dtype=torch.uint8, device=logits.device) if out is None else out
-    check(lib().sx_mtp_pick(_p(logits), logits.numel(), _p(router_err), _p(expert_err), _p(attn_err), _p(emb_err),
-                            _p(out), _s(stream)))
+    if ws is None:
+        check(lib().sx_mtp_pick(_p(logits), logits.numel(), _p(router_err), _p(expert_err), _p(attn_err),
+                                _p(emb_err), _p(out), _s(stream)))
+    else:
+        check(lib().sx_mtp_pick_ws(_p(logits), logits.numel(), _p(router_err), _p(expert_err), _p(attn_err),
+                                   _p(emb_err), _p(out), _p(ws), ws.numel() * ws.element_size(), _s(stream)))
+    return out
+
+
+def mtp_head_pick(x, w, logits, router_err, expert_err, attn_err, emb_err, ws, out=None, stream=None):
+    """The draft head's logits (x BF16 [1, K] against the q4 / q8 head, FP32 [N] into `logits`) and their pick, one
+    launch; `ws` a zeroed device uint8 buffer of mtp_pick_ws_bytes. Returns the 64-byte pick."""
+    out = torch.empty(64, dtype=torch.uint8, device=x.device) if out is None else out
+    assert x.dtype == torch.bfloat16 and x.numel() == w.K and logits.numel() >= w.N
+    check(lib().sx_mtp_head_pick(_p(x), w.view(), w.bits, _p(logits), _p(router_err), _p(expert_err), _p(attn_err),
+                                 _p(emb_err), _p(out), _p(ws), ws.numel() * ws.element_size(), _s(stream)))
     return out
 
 

@@ -96,3 +96,51 @@ def test_draft_head_logits_and_pick():
     b, bv, sv, nan = orc.top2(L[0])
     assert (p.best, p.nan) == (b, nan) and p.best_v == bv and p.second_v == sv
     assert list(p.err)[3:6] == [1, 7, 9] and list(p.err)[:3] == [0, 0, 0]
+
+
+@pytest.mark.parametrize("bits,G,N,K", [(4, 64, 65536, 4096), (4, 64, 1000, 4096), (8, 64, 4100, 2048),
+                                        (4, 128, 37, 1024), (4, 128, 50, 256)])
+def test_mtp_head_pick_matches_linear_then_pick(bits, G, N, K):
+    """sx_mtp_head_pick (the GEMV with the pick fused, or for K = 256 the GEMV then sx_mtp_pick_ws) against
+    sx_linear_q4 / q8 then the single-block sx_mtp_pick: the logits and the 64-byte pick bit for bit, on plain
+    weights, on a tie at the top (two equal rows far apart: the lower id wins) and on a NaN row (flagged). Every call
+    shares one workspace (the count each call leaves at zero)."""
+    import torch
+    rng = np.random.default_rng(N + K + bits)
+    base = util.rand_qweight(rng, bits, N, K, G)
+    rb, gpr = K // (2 if bits == 4 else 1), K // G
+    cases = [base]
+    if N >= 8:
+        t = util.rand_qweight(rng, bits, N, K, G)
+        for a in (t.q, t.scale, t.minv):
+            w = len(a) // N
+            a[(N - 3) * w:(N - 2) * w] = a[5 * w:6 * w]
+        # every other row scaled down, so rows 5 and N - 3 are on top
+        t.scale.reshape(N, gpr)[np.arange(N) % 2 == 0] = util.f32_to_bf16(np.float32(1e-4))
+        t.scale.reshape(N, gpr)[[5, N - 3]] = util.f32_to_bf16(np.float32(0.5))
+        t.minv.reshape(N, gpr)[:] = 0
+        cases.append(t)
+        t = util.rand_qweight(rng, bits, N, K, G)
+        t.scale[(N // 2) * gpr] = 0x7FC0  # NaN: row N / 2
+        cases.append(t)
+    # x > 0: with zero mins the scaled-up rows' logits are the largest
+    x = util.bf16_dev(util.f32_to_bf16(np.abs(rng.standard_normal((1, K))).astype(np.float32) + 0.1))
+    errs = [torch.tensor([i, 2 * i, 3 * i, 0], dtype=torch.int32, device="cuda") for i in (1, 4, 7)]
+    emb = torch.tensor([0x1234_5678_9ABC], dtype=torch.int64, device="cuda")
+    ws = torch.zeros(kx().mtp_pick_ws_bytes(N), dtype=torch.uint8, device="cuda")
+    for ci, hw in enumerate(cases):
+        print(f"bits={bits} G={G} N={N} K={K} case {ci}", flush=True)
+        w = kx().QWeight.upload(hw)
+        ref_L = kx().linear(x, w, out_act=kx().ACT_F32)
+        ref_p = kx().mtp_pick(ref_L[0], *errs, emb)
+        L = torch.full((N,), 7.0, dtype=torch.float32, device="cuda")
+        p = kx().mtp_head_pick(x, w, L, *errs, emb, ws)
+        sync()
+        assert np.array_equal(L.cpu().numpy().view(np.uint32), ref_L[0].cpu().numpy().view(np.uint32)), "logits"
+        assert bytes(p.cpu().numpy()) == bytes(ref_p.cpu().numpy()), "pick"
+        got = kx().pick_from_bytes(p)
+        if ci == 1:
+            assert got.best == 5 and got.best_v == got.second_v and not got.nan
+        if ci == 2:
+            assert got.nan == 1
+    assert not ws[-16:].any().item(), "the count is back at zero"

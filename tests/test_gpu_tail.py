@@ -92,9 +92,21 @@ def test_mtp_pick(n):
     cases.append(np.full(n, np.nan, np.float32))  # all NaN: best 0, flagged
     errs = [torch.tensor([i, 2 * i, 3 * i], dtype=torch.int32, device="cuda") for i in (1, 4, 7)]
     emb = torch.tensor([0x1234_5678_9ABC], dtype=torch.int64, device="cuda")
+    ws = torch.zeros(kx().mtp_pick_ws_bytes(n), dtype=torch.uint8, device="cuda")  # shared by every call below
     for x in cases:
-        out = kx().mtp_pick(util.f32_dev(x), *errs, emb)
+        xd = util.f32_dev(x)
+        out = kx().mtp_pick(xd, *errs, emb)
+        out_ws = kx().mtp_pick(xd, *errs, emb, ws=ws)
+        # unaligned / non-multiple-of-4 rows take the scalar loads
+        out_odd = kx().mtp_pick(xd[1:], *errs, emb, ws=ws) if n > 1 else None
         sync()
+        assert bytes(out_ws.cpu().numpy()) == bytes(out.cpu().numpy()), "many-block pick differs"
+        if out_odd is not None:
+            p1 = kx().pick_from_bytes(out_odd)
+            b1, bv1, sv1, nan1 = orc.top2(x[1:])
+            assert (p1.best, p1.nan) == (b1, nan1)
+            if not nan1:
+                assert np.float32(p1.best_v) == np.float32(bv1) and np.float32(p1.second_v) == np.float32(sv1)
         p = kx().pick_from_bytes(out)
         b, bv, sv, nan = orc.top2(x)
         assert (p.best, p.nan) == (b, nan)
