@@ -92,6 +92,26 @@ def test_topk_workspace_and_reports(L):
     assert L.sx_report_router_error(e, b"x") == sx.SX_OK
 
 
+def test_pick_workspace_contract(L):
+    # the many-block pick's workspace: a 16-byte top-2 for each of up to 256 blocks and the count
+    n = ctypes.c_size_t()
+    assert L.sx_mtp_pick_ws_bytes(65536, ctypes.byref(n)) == 0 and n.value == 256 * 16 + 16
+    assert L.sx_mtp_pick_ws_bytes(0, ctypes.byref(n)) == sx.SX_EINVAL
+    buf = (ctypes.c_uint8 * 8192)()
+    p = ctypes.cast(buf, ctypes.c_void_p).value
+    p16 = (p + 15) // 16 * 16
+    P = lambda o=0: ctypes.c_void_p(p16 + o)
+    rc = L.sx_mtp_pick_ws(P(), 1000, P(), P(), P(), P(), P(), P(64), 4000, None)
+    assert rc == sx.SX_EINVAL and b"need 4112" in L.sx_last_error()
+    rc = L.sx_mtp_pick_ws(P(), 1000, P(), P(), P(), P(), P(), P(8), 4112, None)
+    assert rc == sx.SX_EINVAL and b"16-byte aligned" in L.sx_last_error()
+    w = sx.QView(p16, p16, p16, 16, 128, 64)
+    rc = L.sx_mtp_head_pick(P(), ctypes.byref(w), 5, P(), P(), P(), P(), P(), P(), P(64), 4112, None)
+    assert rc == sx.SX_EINVAL and b"bits = 5" in L.sx_last_error()
+    rc = L.sx_mtp_head_pick(P(), ctypes.byref(w), 4, P(1024), P(), P(), P(), P(), P(), P(64), 100, None)
+    assert rc == sx.SX_EINVAL and b"need 4112" in L.sx_last_error()
+
+
 def test_engine_draft_and_commit_rules():
     """serve/engine.cpp:574-581 (a draft is kept when its top-1 margin reaches mtp_margin and it is no end token; NaN is
     an error) and :612-645 (keep every verify row when all drafts were accepted, else the verified token and the
