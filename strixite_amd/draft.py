@@ -5,7 +5,9 @@ DraftHead is the tail of Qwen4ExpSession::run_mtp / forward_mtp_top2 (runtime/qw
 the MTP layer's collapsed hidden state through the first mtp_vocab rows of the LM head - the Q4 copy
 Qwen4ExpModel::make_draft_head_q4 makes of the Q8 head (runtime/qwen4exp.cpp:192-238, formats/q4_from_q8.hpp), made
 here on the device from the resident Q8 rows - to FP32 logits, then mtp_pick's top-2 with the forward's error words
-in one 64-byte record. The MTP layer itself (attention, hyper-connections) is outside this library.
+in one 64-byte record. The pick runs inside the GEMV's launch (sx_mtp_head_pick: each block keeps the top-2 of the
+logits it writes, the last block to finish merges them), bit-identical to the separate pick. The MTP layer itself
+(attention, hyper-connections) is outside this library.
 
 draft_continues and commit_after_accept are the engine's host-side rules (serve/engine.cpp:574-581, 612-645): whether a
 draft is kept and chained, and which part of the verify the session keeps once the accepted length is known.
