@@ -190,19 +190,26 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) w[nb] = *reinterpret_cast<const uint2 *>(srow[nb] + k);
     };
-    // the span sums of stage st's 64 rows (K step grp): 4 threads a row, 4 slots each (any slot order sums the row)
+    // the span sums of stage st's 64 rows (K step grp): 4 threads a row, 4 chunks each
     auto sum_rows = [&](int st, int grp) __attribute__((always_inline)) {
         const int r = tid >> 2, qd = tid & 3;
         if (!dma_on) return;  // rows 32..63 of a tile of at most 32 slots
-        const unsigned char *xb = xs_at(st) + r * 256 + qd * 64;
+        // chunks 4 qd .. 4 qd + 3 of the row in chunk order (chunk c sits in slot c ^ (r & 15)), so that a slot's
+        // sum does not depend on its position in the tile
+        const uint32_t grp0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)(
+            xs_at(st) + r * 256 + ((qd ^ ((r & 15) >> 2)) * 64));
+        const uint32_t at = grp0 + ((uint32_t)(r & 3) << 4);  // chunk 4 qd + i at at ^ 16 i (grp0 is 64-byte aligned)
         // read in asm: the wait-count pass would otherwise hold these reads for every DMA in flight (it cannot
-        // tell this stage from the one just issued); the step's barrier already covers this stage's DMA
-        const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)xb;
+        // tell this stage from the one just issued); the step's barrier already covers this stage's DMA. One
+        // scratch register forms the other three addresses (a read has taken its address once it has issued).
         uint4 raw[4];
-        asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\tds_read_b128 %2, %4 offset:32\n\t"
-                     "ds_read_b128 %3, %4 offset:48\n\ts_waitcnt lgkmcnt(0)"
-                     : "=v"(raw[0]), "=v"(raw[1]), "=v"(raw[2]), "=v"(raw[3])
-                     : "v"(addr));
+        uint32_t tmp;
+        asm volatile("ds_read_b128 %0, %5\n\t"
+                     "v_xor_b32 %4, 16, %5\n\tds_read_b128 %1, %4\n\t"
+                     "v_xor_b32 %4, 32, %5\n\tds_read_b128 %2, %4\n\t"
+                     "v_xor_b32 %4, 48, %5\n\tds_read_b128 %3, %4\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&v"(raw[0]), "=&v"(raw[1]), "=&v"(raw[2]), "=&v"(raw[3]), "=&v"(tmp)
+                     : "v"(at));
         float sum = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -393,6 +400,264 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         }
 }
 
+// ---------------- down at prefill width: the tile's activations resident ----------------
+// COMBINE with K <= 1024 (the experts' down projection, K = I). gg_kernel pays, for every 256 weight rows, the tile's
+// set-up, the activation DMA of every K step, the pipeline's fill and a barrier a step, and at K = 1024 a block has
+// only 8 K steps to spread them over. Here a block of 16 waves stages its 64-slot tile's activations over the whole
+// K in LDS once (128 KB at K = 1024, in gg_kernel's K-step layout, with gg_kernel's span sums) and then streams chunk
+// after chunk of 512 weight rows against them, a wave 32 rows x the 64 slots (2 v_mfma_f32_32x32x16_bf16 tiles a
+// step): the K loop only reads LDS, so it has no barrier, and four waves a SIMD (a wave's registers fit in 128)
+// hide each other's latencies. The codes and scales of the step two ahead (across chunk ends) and each chunk's
+// scales and mins for the final fold are ordinary loads the compiler waits for. A block takes the chunks
+// [part * n / kPdSplits, (part + 1) * n / kPdSplits) of its tile.
+constexpr int kPdThreads = 1024, kPdWaves = 16, kPdMaxSteps = 8;
+constexpr int kPdChunkRows = kPdWaves * 32;
+constexpr int kPdSumStride = kPdMaxSteps + 4;  // floats a row of the span sums
+constexpr int kPdSplits = 2;                   // blocks a tile
+
+// The step's fold happens in the step: an empty asm that takes the 16 sums as operands (otherwise the compiler moves
+// every step's fold to the chunk's end and keeps all the steps' MFMA results alive, far more than the registers hold).
+__device__ __forceinline__ void pin16(f32x16 &a) {
+    asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
+                 "+v"(a[8]), "+v"(a[9]), "+v"(a[10]), "+v"(a[11]), "+v"(a[12]), "+v"(a[13]), "+v"(a[14]), "+v"(a[15]));
+}
+
+template <int NK, bool TWO>
+__device__ __forceinline__ void pd_run(const Params &p, const unsigned char *xs, const float *xsum,
+                                       const int64_t *s_out, int T, int bucket, int c0, int c1) {
+    using Win = std::conditional_t<NK == 8, uint4, uint2>;  // a row's NK BF16 scales (or mins)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int j = lane & 31, h = lane >> 5;
+    const int64_t N = p.N, rowbytes = p.K / 2;
+    // the lane's weight row of chunk c (past the end: the last chunk again, loaded and never used), clamped into
+    // the expert
+    auto row_of = [&](int c) -> int64_t {
+        c = min(c, c1 - 1);
+        const int64_t n = (int64_t)c * kPdChunkRows + wave * 32 + j;
+        return (int64_t)bucket * N + (n < N ? n : N - 1);
+    };
+    uint4 cw[2][2];     // [ring slot][half]: the step's 32 bytes of codes
+    uint32_t sc[2];     // [ring slot]: its scale
+    auto issue = [&](int64_t row, int k, int RS, int half) {
+        cw[RS][half] = *reinterpret_cast<const uint4 *>(p.q + row * rowbytes + h * 32 + k * kSpanBytes + half * 16);
+        if (half == 1) sc[RS] = p.scale[row * NK + k];
+    };
+    Win wsc, wmn;  // the chunk's scales and mins for the final fold (loaded at its third step)
+    auto word = [](const Win &w, int s) -> uint32_t {
+        if constexpr (NK == 8) return qmm::detail::dword(w, s >> 1);
+        else return s < 2 ? w.x : w.y;
+    };
+    auto bf = [&](const Win &w, int s) {
+        const uint32_t d = word(w, s);
+        return __uint_as_float((s & 1) ? (d & 0xFFFF0000u) : (d << 16));
+    };
+    {
+        const int64_t r0 = row_of(c0);
+        issue(r0, 0, 0, 0), issue(r0, 0, 0, 1), issue(r0, 1, 1, 0), issue(r0, 1, 1, 1);
+    }
+    // LDS address of the lane's A fragment of MFMA step kk, K step k, half tb: a_base[tb] ^ (kk << 4) plus the
+    // stage (the row's slot kk ^ (row & 15), as (h * 8 + kk) ^ (row & 15) = (h * 8 ^ (row & 15)) ^ kk)
+    uint32_t a_base[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+        const int row = tb * 32 + j;
+        a_base[tb] = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)(
+                         xs + row * 256 + (((h * 8) ^ (row & 15)) * 16));
+    }
+    auto chunk = [&](int c) __attribute__((always_inline)) {
+        const int64_t rc = row_of(c), rn = row_of(c + 1);
+        f32x16 acc[2] = {f32x16{}, f32x16{}};
+        auto kstep = [&](auto k_tag) __attribute__((always_inline)) {
+            constexpr int k = decltype(k_tag)::value, RS = k & 1;
+            constexpr int kn = (k + 2) % NK;  // the step whose loads this one issues: of this chunk or the next
+            const int64_t rl = k + 2 < NK ? rc : rn;
+            if constexpr (k == (NK == 8 ? 2 : 1)) {
+                wsc = *reinterpret_cast<const Win *>(p.scale + rc * NK);
+                wmn = *reinterpret_cast<const Win *>(p.minv + rc * NK);
+            }
+            // opaque to the compiler: the A addresses below are formed in the step (hoisted, one for every MFMA
+            // step and half would hold 16 registers throughout)
+            uint32_t ab0 = a_base[0], ab1 = a_base[1];
+            asm volatile("" : "+v"(ab0), "+v"(ab1));
+            f32x16 D[2];
+            bf16x8 aop[2][2];  // [buffer][tb], one MFMA step ahead
+            auto load_a = [&](int kk, bf16x8 (&a)[2]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb) {
+                    if (tb == 1 && !TWO) continue;
+                    const uint32_t ad = ((tb == 0 ? ab0 : ab1) ^ (uint32_t)(kk << 4)) + k * kStageBytes;
+                    a[tb] = *reinterpret_cast<const __attribute__((address_space(3))) bf16x8 *>((uintptr_t)ad);
+                }
+            };
+            load_a(0, aop[0]);
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+#pragma unroll
+                for (int kq = 0; kq < 4; ++kq) {
+                    const int kk = half * 4 + kq;
+                    if (kk < 7) load_a(kk + 1, aop[(kk + 1) & 1]);
+                    const bf16x8 bop = codes_nat(qmm::detail::dword(cw[RS][half], kq));
+#pragma unroll
+                    for (int tb = 0; tb < 2; ++tb) {
+                        if (tb == 1 && !TWO) continue;
+                        D[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop[kk & 1][tb], bop, kk == 0 ? f32x16{} : D[tb],
+                                                                        0, 0, 0);
+                    }
+                }
+                if (half == 0) issue(rl, kn, RS, 0);
+            }
+            const float s_ = __uint_as_float(sc[RS] << 16);
+            issue(rl, kn, RS, 1);
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                if (tb == 1 && !TWO) continue;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[tb][v] = fmaf(s_, D[tb][v], acc[tb][v]);
+                pin16(acc[tb]);
+            }
+        };
+        [&]<int... Ks>(std::integer_sequence<int, Ks...>) {
+            ((kstep(std::integral_constant<int, Ks>{}), __builtin_amdgcn_sched_barrier(0)), ...);
+        }(std::make_integer_sequence<int, NK>{});
+        // (m - 128 s)[row] * sum x[slot] over the spans on the MFMA, as gg_kernel's (three BF16 terms a side)
+        auto split3 = [](const float (&v)[8], bf16x8 (&t)[3]) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const __bf16 a = (__bf16)v[e];
+                const float r1 = v[e] - (float)a;
+                const __bf16 b = (__bf16)r1;
+                t[0][e] = a, t[1][e] = b, t[2][e] = (__bf16)(r1 - (float)b);
+            }
+        };
+        {
+            bf16x8 bt[3];
+            float cmv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)  // this lane's 8 spans are h * 8 ..: NK <= 8, so lanes of h = 1 hold none
+                cmv[e] = (h == 0 && e < NK) ? fmaf(-128.f, bf(wsc, e & (NK - 1)), bf(wmn, e & (NK - 1))) : 0.f;
+            split3(cmv, bt);
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                if (tb == 1 && !TWO) continue;
+                float xv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = (h == 0 && e < NK) ? xsum[(tb * 32 + j) * kPdSumStride + e] : 0.f;
+                bf16x8 at[3];
+                split3(xv, at);
+#pragma unroll
+                for (int pa = 0; pa < 3; ++pa)
+#pragma unroll
+                    for (int pb = 0; pb < 3 - pa; ++pb)
+                        acc[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(at[pa], bt[pb], acc[tb], 0, 0, 0);
+            }
+        }
+        // FP32 partials: lane value v = slot tb * 32 + 8 (v / 4) + 4 h + v % 4, row j of the wave's 32. The slots'
+        // output rows are read here, from an address the compiler cannot see is the same every chunk (hoisted out
+        // of the chunk loop, the 32 row offsets would hold 64 registers throughout)
+        const int64_t feat = (int64_t)c * kPdChunkRows + wave * 32 + j;
+        uint32_t so = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const int64_t *)s_out;
+        int Tc = T, hc = h;  // likewise the slot bounds (hoisted: 32 masks in scalar registers)
+        asm volatile("" : "+v"(so), "+s"(Tc), "+v"(hc));
+        const __attribute__((address_space(3))) int64_t *outs =
+            reinterpret_cast<const __attribute__((address_space(3))) int64_t *>((uintptr_t)so);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int r = tb * 32 + 8 * (v / 4) + 4 * hc + v % 4;
+                if (r < Tc && feat < N) static_cast<float *>(p.y)[outs[r] * N + feat] = acc[tb][v];
+            }
+    };
+    for (int c = c0; c < c1; ++c) chunk(c);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the block exits
+}
+
+__global__ void __launch_bounds__(kPdThreads, 1) gg_down_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) unsigned char xs[kPdMaxSteps * kStageBytes];
+    __shared__ __attribute__((aligned(16))) float xsum[kBM * kPdSumStride];  // [slot][span]
+    __shared__ int64_t s_xrow[kBM], s_out[kBM];
+    __shared__ int s_T, s_bucket;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t K = p.K, N = p.N;
+    const int E = (int)p.E, nk = (int)(K / kSpan);
+    const int u = (int)(blockIdx.x / kPdSplits), part = (int)(blockIdx.x % kPdSplits);
+
+    if (tid < 64) {  // the tile: bucket, slots (gg_kernel's lookup)
+        const int32_t *ws = p.ws;
+        const int32_t n_wt = ws[3], S = ws[1];
+        int T = 0, bucket = -1;
+        if (u < n_wt) {
+            const int32_t *offsets = ws + 4, *slots = offsets + E + 2;
+            const int64_t Tmax = (int64_t)S / 16 + E + 2, WTmax = (int64_t)S / 64 + E + 2;
+            const int32_t *wtile_bucket = slots + S + 2 * Tmax, *wtile_start = wtile_bucket + WTmax;
+            bucket = wtile_bucket[u];
+            const int32_t st = wtile_start[u];
+            T = min(kBM, offsets[bucket + 1] - st);
+            if (lane < T) {
+                const int64_t slot = slots[st + lane];
+                s_xrow[lane] = slot * K;
+                s_out[lane] = slot;
+            }
+        }
+        if (lane == 0) s_T = T, s_bucket = bucket;
+    }
+    __syncthreads();
+    const int T = __builtin_amdgcn_readfirstlane(s_T), bucket = __builtin_amdgcn_readfirstlane(s_bucket);
+    if (T == 0) return;
+    const int nchunk = (int)((N + kPdChunkRows - 1) / kPdChunkRows);
+    const int c0 = part * nchunk / kPdSplits, c1 = (part + 1) * nchunk / kPdSplits;
+    if (c0 >= c1) return;
+    if (bucket == E) {  // invalid ids (reported by the grouping): NaN rows, never an out-of-range weight read
+        const int64_t f0 = (int64_t)c0 * kPdChunkRows, f1 = min((int64_t)c1 * kPdChunkRows, N);
+        for (int64_t i = tid; i < (int64_t)T * (f1 - f0); i += kPdThreads) {
+            const int r = (int)(i / (f1 - f0));
+            static_cast<float *>(p.y)[s_out[r] * N + f0 + i % (f1 - f0)] = qnan();
+        }
+        return;
+    }
+    if (tid >= T && tid < kBM) s_xrow[tid] = s_xrow[T - 1];  // rows past T: row T - 1 again, never stored
+    __syncthreads();
+
+    // the tile's activations over the whole K into LDS: chunk c8 (8 BF16) of row r to K step c8 / 16, slot
+    // (c8 % 16) ^ (r % 16) of the row (gg_kernel's DMA layout); all loads go out first
+    constexpr int kPer = (kPdMaxSteps * kSpan / 8 * kBM + kPdThreads - 1) / kPdThreads;  // 8
+    const int chunks8 = (int)(K / 8), n_items = kBM * chunks8;
+    uint4 xv[kPer];
+#pragma unroll
+    for (int b = 0; b < kPer; ++b) {
+        const int i = min(b * kPdThreads + tid, n_items - 1);
+        xv[b] = *reinterpret_cast<const uint4 *>(p.x + s_xrow[i / chunks8] + (int64_t)(i % chunks8) * 8);
+    }
+#pragma unroll
+    for (int b = 0; b < kPer; ++b) {
+        const int i = b * kPdThreads + tid;
+        if (i < n_items) {
+            const int r = i / chunks8, c8 = i % chunks8;
+            *reinterpret_cast<uint4 *>(xs + (c8 >> 4) * kStageBytes + r * 256 + (((c8 & 15) ^ (r & 15)) * 16)) = xv[b];
+        }
+    }
+    __syncthreads();
+    // the span sums, as gg_kernel's: 4 threads a (row, span), 4 chunks each in chunk order, then summed across the 4
+    for (int it = tid; it < nk * kBM * 4; it += kPdThreads) {
+        const int g = it >> 8, r = (it >> 2) & (kBM - 1), qd = it & 3;
+        const unsigned char *grp0 = xs + g * kStageBytes + r * 256 + ((qd ^ ((r & 15) >> 2)) * 64);
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // chunk 4 qd + i, in slot (4 qd + i) ^ (r & 15)
+            float v[8];
+            qmm::detail::unpack8(*reinterpret_cast<const uint4 *>(grp0 + ((i ^ (r & 3)) * 16)), v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += v[e];
+        }
+        sum = qmm::detail::group_sum_c<4>(sum);
+        if (qd == 0) xsum[r * kPdSumStride + g] = sum;
+    }
+    __syncthreads();
+    const bool two = T > 32;
+    if (nk == 8) two ? pd_run<8, true>(p, xs, xsum, s_out, T, bucket, c0, c1) : pd_run<8, false>(p, xs, xsum, s_out, T, bucket, c0, c1);
+    else two ? pd_run<4, true>(p, xs, xsum, s_out, T, bucket, c0, c1) : pd_run<4, false>(p, xs, xsum, s_out, T, bucket, c0, c1);
+}
+
 template <int MODE, typename TY>
 hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
     hipLaunchKernelGGL((gg_kernel<MODE, TY>), grid, dim3(kThreads), 0, stream, p);
@@ -426,7 +691,12 @@ hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int
         e = out_act == SX_ACT_F32 ? go<qmm::GATHER, float>(p, grid, stream) : go<qmm::GATHER, uint16_t>(p, grid, stream);
         break;
     default:
-        e = go<qmm::COMBINE, float>(p, grid, stream);
+        if (p.K <= kPdMaxSteps * kSpan && (p.K / kSpan == 8 || p.K / kSpan == 4)) {  // the down projection
+            hipLaunchKernelGGL(gg_down_kernel, dim3((unsigned)(wtiles * kPdSplits)), dim3(kPdThreads), 0, stream, p);
+            e = hipGetLastError();
+        } else {
+            e = go<qmm::COMBINE, float>(p, grid, stream);
+        }
     }
     return e;
 }

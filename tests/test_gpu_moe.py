@@ -227,9 +227,11 @@ def test_grouped_matches_per_slot_oracle(M, A, E, I, d):
     assert err.cpu().numpy()[0] == 0
 
 
-@pytest.mark.parametrize("M,A,E,I,d", [(96, 4, 8, 512, 512), (40, 3, 5, 512, 2048), (64, 2, 3, 1024, 1024)])
+@pytest.mark.parametrize("M,A,E,I,d", [(96, 4, 8, 512, 512), (40, 3, 5, 512, 2048), (64, 2, 3, 1024, 1024),
+                                       (48, 2, 4, 2048, 512)])
 def test_prefill_grouped_mfma_matches_oracle(M, A, E, I, d):
-    """Prefill width (M >= 32 takes the 64-slot x 128-row MFMA kernel): gather, SwiGLU gather and combine against the
+    """Prefill width (M >= 32 takes the 64-slot x 128-row MFMA kernel; the combine at I = 512 or 1024 the kernel
+    with the tile's activations resident, at I = 2048 the 64-slot one): gather, SwiGLU gather and combine against the
     oracle, with one bucket far over 64 slots (several wide tiles), one of exactly 64, and an invalid id (NaN rows,
     error words from the grouping)."""
     import torch

@@ -52,7 +52,16 @@ def test_config4_prefill_layer_full_size():
     sync()
     assert torch.equal(h.view(torch.int16), h2.view(torch.int16)), "grouped gate_up differs between two runs"
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), "grouped down + combine differs between two runs"
-    del h2, y2
+    # a second grouping places the slots of a bucket in another order (the counting sort's atomics): a slot's results
+    # must not depend on its place in its tile
+    print("config 4: regrouped (slot order within the buckets changes)", flush=True)
+    ws3, _ = kx().group_routes(ids, E)
+    h3 = kx().gather_grouped(x, gu, E, ws3, M, k, swiglu=True)
+    y3 = kx().combine_grouped(h3, dn, E, ids, coef, ws3)
+    sync()
+    assert torch.equal(h.view(torch.int16), h3.view(torch.int16)), "grouped gate_up depends on the slot order"
+    assert torch.equal(y.view(torch.int16), y3.view(torch.int16)), "grouped down + combine depends on the slot order"
+    del h2, y2, h3, y3, ws3
 
     xh = util.host_bits(x)
     util.assert_close(raw.cpu().numpy(), orc.linear_f32w(xh, Wr.cpu().numpy()), tol=1e-5, what="router logits")
