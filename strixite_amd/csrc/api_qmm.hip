@@ -87,6 +87,11 @@ int linear(const char *fn, int bits, const void *x, const sx_qview *w, void *y, 
         SX_HIP(dks::launch(bits, w->G, act, out_act, d, device_cus(), stream_of(stream)), fn);
         return SX_OK;
     }
+    if (M >= gg::kPrefillMinTokens && gg::eligible(bits, w->G, w->K, act) && aligned(w->scale, 4) &&
+        aligned(w->minv, 4)) {  // prefill width: the grouped kernel's MFMA tiles, the tokens as one bucket
+        SX_HIP(gg::launch_dense(x, w, y, M, out_act, stream_of(stream)), fn);
+        return SX_OK;
+    }
     const int nsplit = act == SX_ACT_F32 ? 3 : 1;
     const int rows = rows_that_fit(bits, nsplit, w->K, w->G, (int)(M < 16 ? M : 16));
     SX_CHECK(qmm::lds_bytes(bits, nsplit, w->K, w->G, rows, 1) <= 160 * 1024, fn, " K = ", w->K,

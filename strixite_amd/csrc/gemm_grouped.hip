@@ -45,6 +45,7 @@ struct Params {
     int64_t A, N, K;  // slots a token; rows an expert (SWIGLU: 2I); K
     int64_t E;
     int nrb;  // row blocks
+    int64_t dense_M;  // > 0: a dense linear (GATHER) over dense_M token rows, tile u = tokens 64 u .. (no workspace)
 };
 
 // The 1-D grid in groups of 8 tiles x nrb row blocks, row-block-major inside a group: the row blocks of a tile get
@@ -96,7 +97,13 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     const int E = (int)p.E;
 
     // ---- the 64-slot tile: bucket, slots (wave 0, lane r fills row r) ----
-    if (tid < 64) {
+    if (tid < 64 && p.dense_M > 0) {  // a dense linear: one "bucket" (the weight), the tokens in order
+        const int u = tile_of(blockIdx.x, p.nrb);
+        const int64_t t0 = (int64_t)u * kBM;
+        const int T = t0 < p.dense_M ? (int)min((int64_t)kBM, p.dense_M - t0) : 0;
+        if (lane < T) s_xrow[lane] = (t0 + lane) * K, s_out[lane] = t0 + lane;
+        if (lane == 0) s_T = T, s_bucket = 0;
+    } else if (tid < 64) {
         const int32_t *ws = p.ws;
         const int32_t n_wt = ws[3], S = ws[1];
         int T = 0, bucket = -1;
@@ -665,6 +672,17 @@ hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
 }
 
 }  // namespace
+
+hipError_t launch_dense(const void *x, const sx_qview *w, void *y, int64_t M, int out_act, hipStream_t stream) {
+    Params p{};
+    p.x = static_cast<const uint16_t *>(x), p.q = static_cast<const uint8_t *>(w->q);
+    p.scale = static_cast<const uint16_t *>(w->scale), p.minv = static_cast<const uint16_t *>(w->minv);
+    p.y = y, p.ws = nullptr, p.A = 1, p.N = w->N, p.K = w->K, p.E = 1, p.dense_M = M;
+    p.nrb = (int)((p.N + kWaves * 64 - 1) / (kWaves * 64));
+    const int64_t tiles = (M + kBM - 1) / kBM;
+    const dim3 grid((unsigned)((tiles + 7) / 8 * 8 * p.nrb));
+    return out_act == SX_ACT_F32 ? go<qmm::GATHER, float>(p, grid, stream) : go<qmm::GATHER, uint16_t>(p, grid, stream);
+}
 
 bool eligible(int bits, int64_t G, int64_t K, int act) {
     return bits == 4 && G == 128 && K % (4 * kSpan) == 0 && K <= kSpan * kMaxGroups && act == SX_ACT_BF16;

@@ -112,11 +112,15 @@ def test_config4_prefill_layer_full_size():
     util.assert_close(util.host_bits(y)[toks], ref_y, what="config 4 y (sampled tokens)")
 
 
-@pytest.mark.parametrize("bits,G,act,out_act", [(4, 128, orc.BF16, orc.BF16), (8, 64, orc.BF16, orc.F32),
-                                               (4, 128, orc.F32, orc.F32)])
-def test_dense_linear_prefill_width(bits, G, act, out_act):
-    """linear_q4 / linear_q8 at M = 2048 (the prefill-width route *_wmma callers take) against the oracle."""
-    M, N, K = 2048, 384, 4096
+@pytest.mark.parametrize("bits,G,act,out_act,M,K", [(4, 128, orc.BF16, orc.BF16, 2048, 4096),
+                                                     (4, 128, orc.BF16, orc.F32, 2000, 2048),
+                                                     (4, 128, orc.BF16, orc.BF16, 33, 512),
+                                                     (8, 64, orc.BF16, orc.F32, 2048, 4096),
+                                                     (4, 128, orc.F32, orc.F32, 2048, 4096)])
+def test_dense_linear_prefill_width(bits, G, act, out_act, M, K):
+    """linear_q4 / linear_q8 at prefill width (the route *_wmma callers take; q4 G = 128 with BF16 x on the grouped
+    kernel's MFMA tiles, a partial last tile of tokens and of rows included) against the oracle."""
+    N = 384
     rng = np.random.default_rng(bits * 10 + act)
     w = util.rand_qweight(rng, bits, N, K, G)
     x = rng.standard_normal((M, K)).astype(np.float32)
