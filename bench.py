@@ -361,6 +361,14 @@ def extra_configs(out):
                      "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del reps
     # config 4: the MoE layer at prefill width, M = 2048, Zipf-skewed routing; grouped MFMA experts
+    # a dense q4 linear at prefill width (the route linear_q4_wmma's callers take), 4096 x 4096 at M = 2048
+    w = syn.qweight(4, 4096, 4096, 128, seed=70)
+    x = syn.activations(2048, 4096, seed=71)
+    y = torch.empty((2048, 4096), dtype=torch.bfloat16, device="cuda")
+    ms = time_window(lambda i: kx.linear(x, w, y=y), min_launches=20, min_ms=20.0)
+    res["prefill_dense_q4_4096x4096_M2048"] = {"us": round(ms * 1e3, 1),
+                                               "mfma_frac": round(2.0 * 2048 * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
+    del w, x, y
     res["cfg4_prefill_layer"] = prefill_layer()
     res["cfg5_verify_tail"] = verify_tail()
     res["mtp_draft_head"] = draft_head()
