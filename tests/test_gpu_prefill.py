@@ -114,7 +114,7 @@ def test_config4_prefill_layer_full_size():
 
 @pytest.mark.parametrize("bits,G,act,out_act,M,K", [(4, 128, orc.BF16, orc.BF16, 2048, 4096),
                                                      (4, 128, orc.BF16, orc.F32, 2000, 2048),
-                                                     (4, 128, orc.BF16, orc.BF16, 33, 512),
+                                                     (4, 128, orc.BF16, orc.BF16, 257, 512),
                                                      (8, 64, orc.BF16, orc.F32, 2048, 4096),
                                                      (4, 128, orc.F32, orc.F32, 2048, 4096)])
 def test_dense_linear_prefill_width(bits, G, act, out_act, M, K):
