@@ -369,6 +369,14 @@ def extra_configs(out):
     res["prefill_dense_q4_4096x4096_M2048"] = {"us": round(ms * 1e3, 1),
                                                "mfma_frac": round(2.0 * 2048 * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
     del w, x, y
+    # the same at q8 G = 64 (linear_q8_wmma's callers)
+    w = syn.qweight(8, 4096, 4096, 64, seed=72)
+    x = syn.activations(2048, 4096, seed=73)
+    y = torch.empty((2048, 4096), dtype=torch.bfloat16, device="cuda")
+    ms = time_window(lambda i: kx.linear(x, w, y=y), min_launches=20, min_ms=20.0)
+    res["prefill_dense_q8_4096x4096_M2048"] = {"us": round(ms * 1e3, 1),
+                                               "mfma_frac": round(2.0 * 2048 * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
+    del w, x, y
     res["cfg4_prefill_layer"] = prefill_layer()
     res["cfg5_verify_tail"] = verify_tail()
     res["mtp_draft_head"] = draft_head()

@@ -36,6 +36,26 @@ constexpr int kLoadsPerStep = kDmaPerWave + 6;  // most a step issues: + 4 code 
 constexpr int kMaxGroups = 32;  // K <= 4096: the span sums of every step stay in LDS
 constexpr int kSumStride = kMaxGroups + 4;  // floats a row (16-byte aligned, rows 4 banks apart)
 
+// gg_kernel's K-step layout for q4 (G = 128) and q8 (G = 64) weights: one quantization group a K step (64 bytes of a
+// weight row either way), the step's activation rows in 16-byte chunks, chunk c of row r in slot c ^ swz(r). The
+// swizzle makes the 16 rows a quarter-wave's MFMA operand reads touch distinct banks (q4: 256-byte rows, 16 chunks;
+// q8: 128-byte rows, two to the 256 bytes of the banks, so rows r and r + 1 share a swizzle and differ in half).
+template <int BITS>
+struct Lay {
+    static constexpr int kSpan = BITS == 4 ? 128 : 64;  // codes a K step
+    static constexpr int kChunks = kSpan / 8;             // 16-byte activation chunks a row a step
+    static constexpr int kRowBytes = kSpan * 2;
+    static constexpr int kStageBytes = kBM * kRowBytes;   // 16 KB / 8 KB
+    static constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 4 / 2
+    static constexpr int kLoadsPerStep = kDmaPerWave + 6;
+    static constexpr int kMaxGroups = 4096 / kSpan;        // K <= 4096
+    static constexpr int kSumStride = kMaxGroups + 4;
+    static constexpr int kKk = kSpan / 16;                 // MFMAs (k = 16) a step: 8 / 4
+    static constexpr float kOff = BITS == 4 ? 128.f : 0.f;  // the operand is code + kOff
+    static constexpr int kStageAlign = BITS == 4 ? 16 : 128;
+    __device__ static int swz(int r) { return BITS == 4 ? (r & 15) : ((r >> 1) & 7); }
+};
+
 struct Params {
     const uint16_t *x;  // BF16 activations [tokens or slots, K]
     const uint8_t *q;
@@ -77,15 +97,30 @@ __device__ __forceinline__ bf16x8 codes_nat(uint32_t d) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
+// Operand of 8 q8 codes (two dwords, code order = byte order) as BF16: each byte to FP32 (exact) and the upper
+// halves of two FP32 values into one dword.
+__device__ __forceinline__ bf16x8 codes8(uint32_t d0, uint32_t d1) {
+    auto pair = [](uint32_t d, int b) {
+        const uint32_t lo = __float_as_uint((float)((d >> (8 * b)) & 0xFFu));
+        const uint32_t hi = __float_as_uint((float)((d >> (8 * b + 8)) & 0xFFu));
+        return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+    };
+    const uint4 v{pair(d0, 0), pair(d0, 2), pair(d1, 0), pair(d1, 2)};
+    return __builtin_bit_cast(bf16x8, v);
+}
+
 __device__ __forceinline__ void dma16(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
 }
 
-template <int MODE, typename TY>
+template <int MODE, typename TY, int BITS>
 __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
+    using L = Lay<BITS>;
+    constexpr int kSpan = L::kSpan, kStageBytes = L::kStageBytes, kDmaPerWave = L::kDmaPerWave,
+                  kLoadsPerStep = L::kLoadsPerStep, kSumStride = L::kSumStride;
     // One array a stage, so that the wait-count pass tells a stage's DMA apart from the others'.
-    __shared__ __attribute__((aligned(16))) unsigned char x0[kStageBytes], x1[kStageBytes], x2[kStageBytes],
-        x3[kStageBytes];
+    __shared__ __attribute__((aligned(L::kStageAlign))) unsigned char x0[kStageBytes], x1[kStageBytes],
+        x2[kStageBytes], x3[kStageBytes];
     __shared__ __attribute__((aligned(16))) float xsum[kBM * kSumStride];  // [slot][span]
     __shared__ int64_t s_xrow[kBM], s_out[kBM];
     __shared__ int s_T, s_bucket;
@@ -143,7 +178,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     __syncthreads();
 
     // ---- this lane's two weight rows (nb = 0, 1), clamped into the expert (stores are masked) ----
-    const int64_t rowbytes = K / 2, ngroups = K / kSpan;
+    const int64_t rowbytes = BITS == 4 ? K / 2 : K, ngroups = K / kSpan;
     const uint8_t *qrow[2];
     const uint16_t *srow[2], *mrow[2];
     int64_t feat[2];
@@ -159,13 +194,15 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         srow[nb] = p.scale + row * ngroups;
         mrow[nb] = p.minv + row * ngroups;
     }
-    // Activation DMA: instruction I (0..15) covers tile rows 4I .. 4I + 3; lane l writes row 4I + l / 16, chunk
-    // (l & 15) ^ (row & 15), so slot s of a row holds chunk s ^ (row & 15). This wave issues I = 4 wave + i.
+    // Activation DMA: instruction I covers kDmaRows tile rows from kDmaRows I; lane l writes row kDmaRows I +
+    // l / kChunks, chunk (l % kChunks) ^ swz(row), so slot s of a row holds chunk s ^ swz(row) (q4: 16 instructions
+    // of 4 rows; q8: 8 of 8). This wave issues I = kDmaPerWave wave + i.
+    constexpr int kChunks = L::kChunks, kDmaRows = 64 / kChunks;
     const uint16_t *xl[kDmaPerWave];
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-        const int r = 4 * (kDmaPerWave * wave + i) + (lane >> 4);
-        xl[i] = p.x + s_xrow[r] + (((lane & 15) ^ (r & 15)) * 8);
+        const int r = kDmaRows * (kDmaPerWave * wave + i) + lane / kChunks;
+        xl[i] = p.x + s_xrow[r] + (((lane % kChunks) ^ L::swz(r)) * 8);
     }
     auto xs_at = [&](int st) -> unsigned char * { return st == 0 ? x0 : st == 1 ? x1 : st == 2 ? x2 : x3; };
     const int nk = (int)(K / kSpan);
@@ -201,6 +238,28 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     auto sum_rows = [&](int st, int grp) __attribute__((always_inline)) {
         const int r = tid >> 2, qd = tid & 3;
         if (!dma_on) return;  // rows 32..63 of a tile of at most 32 slots
+        if constexpr (BITS == 8) {
+            // chunks 2 qd, 2 qd + 1 in chunk order: slots (2 qd) ^ swz(r) and that ^ 1 (the row is 128-byte aligned)
+            const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)(
+                xs_at(st) + r * 128 + (((2 * qd) ^ L::swz(r)) * 16));
+            uint4 raw[2];
+            uint32_t tmp;
+            asm volatile("ds_read_b128 %0, %3\n\t"
+                         "v_xor_b32 %2, 16, %3\n\tds_read_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(raw[0]), "=&v"(raw[1]), "=&v"(tmp)
+                         : "v"(at));
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                float v[8];
+                qmm::detail::unpack8(raw[i], v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sum += v[e];
+            }
+            sum = qmm::detail::group_sum_c<4>(sum);
+            if (qd == 0 && grp < nk) xsum[r * kSumStride + grp] = sum;
+            return;
+        }
         // chunks 4 qd .. 4 qd + 3 of the row in chunk order (chunk c sits in slot c ^ (r & 15)), so that a slot's
         // sum does not depend on its position in the tile
         const uint32_t grp0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)(
@@ -248,19 +307,24 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
             for (int tb = 0; tb < 2; ++tb) {
                 if (tb == 1 && !TWO) continue;
                 const int row = tb * 32 + j;
-                a[tb] = *reinterpret_cast<const bf16x8 *>(xb + row * 256 + (((h * 8 + kk) ^ (row & 15)) * 16));
+                a[tb] = *reinterpret_cast<const bf16x8 *>(xb + row * L::kRowBytes +
+                                                          (((h * (kChunks / 2) + kk) ^ L::swz(row)) * 16));
             }
         };
         load_a(0, aop[0]);
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
 #pragma unroll
-            for (int kq = 0; kq < 4; ++kq) {
-                const int kk = half * 4 + kq;
-                if (kk < 7) load_a(kk + 1, aop[(kk + 1) & 1]);
+            for (int kq = 0; kq < L::kKk / 2; ++kq) {
+                const int kk = half * (L::kKk / 2) + kq;
+                if (kk < L::kKk - 1) load_a(kk + 1, aop[(kk + 1) & 1]);
                 bf16x8 bop[2];
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) bop[nb] = codes_nat(qmm::detail::dword(cw[RS][nb][half], kq));
+                for (int nb = 0; nb < 2; ++nb) {
+                    const uint4 &c = cw[RS][nb][half];
+                    if constexpr (BITS == 4) bop[nb] = codes_nat(qmm::detail::dword(c, kq));
+                    else bop[nb] = codes8(qmm::detail::dword(c, 2 * kq), qmm::detail::dword(c, 2 * kq + 1));
+                }
 #pragma unroll
                 for (int tb = 0; tb < 2; ++tb) {
                     if (tb == 1 && !TWO) continue;
@@ -360,7 +424,8 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
             float cmv[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                cmv[e] = gl + e < nk ? fmaf(-128.f, bf16_to_f32(srow[nb][gl + e]), bf16_to_f32(mrow[nb][gl + e])) : 0.f;
+                cmv[e] = gl + e < nk ? fmaf(-L::kOff, bf16_to_f32(srow[nb][gl + e]), bf16_to_f32(mrow[nb][gl + e]))
+                                     : 0.f;
             split3(cmv, bt[nb]);
         }
 #pragma unroll
@@ -665,9 +730,9 @@ __global__ void __launch_bounds__(kPdThreads, 1) gg_down_kernel(Params p) {
     else two ? pd_run<4, true>(p, xs, xsum, s_out, T, bucket, c0, c1) : pd_run<4, false>(p, xs, xsum, s_out, T, bucket, c0, c1);
 }
 
-template <int MODE, typename TY>
+template <int MODE, typename TY, int BITS = 4>
 hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
-    hipLaunchKernelGGL((gg_kernel<MODE, TY>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((gg_kernel<MODE, TY, BITS>), grid, dim3(kThreads), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -681,11 +746,19 @@ hipError_t launch_dense(const void *x, const sx_qview *w, void *y, int64_t M, in
     p.nrb = (int)((p.N + kWaves * 64 - 1) / (kWaves * 64));
     const int64_t tiles = (M + kBM - 1) / kBM;
     const dim3 grid((unsigned)((tiles + 7) / 8 * 8 * p.nrb));
+    if (w->G == 64)  // q8
+        return out_act == SX_ACT_F32 ? go<qmm::GATHER, float, 8>(p, grid, stream)
+                                     : go<qmm::GATHER, uint16_t, 8>(p, grid, stream);
     return out_act == SX_ACT_F32 ? go<qmm::GATHER, float>(p, grid, stream) : go<qmm::GATHER, uint16_t>(p, grid, stream);
 }
 
 bool eligible(int bits, int64_t G, int64_t K, int act) {
     return bits == 4 && G == 128 && K % (4 * kSpan) == 0 && K <= kSpan * kMaxGroups && act == SX_ACT_BF16;
+}
+
+bool eligible_dense(int bits, int64_t G, int64_t K, int act) {
+    if (bits == 8) return G == 64 && K % (4 * Lay<8>::kSpan) == 0 && K <= 4096 && act == SX_ACT_BF16;
+    return eligible(bits, G, K, act);
 }
 
 hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int32_t *ws, int64_t M, int64_t A,

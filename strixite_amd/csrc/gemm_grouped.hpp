@@ -12,8 +12,10 @@ bool eligible(int bits, int64_t G, int64_t K, int act);
 // Tokens from which a dense q4 linear takes the grouped kernel's tiles (launch_dense): below, its few tiles leave
 // the chip idle and qmm's dense mode is faster (4096 x 4096: 41 against 61 us at M = 128, 73 against 62 at 256).
 constexpr int64_t kDenseMinTokens = 256;
+// The dense linears the tiles take: eligible's q4, and q8 (G = 64, K % 256 == 0, K <= 4096, BF16 x).
+bool eligible_dense(int bits, int64_t G, int64_t K, int act);
 // A dense linear at prefill width on the same tiles: y [M, w->N] (BF16 or FP32) = x [M, K] (BF16) . deq(w)^T, tile u
-// = tokens 64 u .. 64 u + 63 (eligible(4, G, K, BF16)).
+// = tokens 64 u .. 64 u + 63 (eligible_dense(bits, G, K, BF16)).
 hipError_t launch_dense(const void *x, const sx_qview *w, void *y, int64_t M, int out_act, hipStream_t stream);
 // mode: qmm::SWIGLU (h [S, N/2]), qmm::GATHER (y [S, N]), qmm::COMBINE (FP32 partials [S, N]); N = w->N / E.
 hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int32_t *ws, int64_t M, int64_t A,
