@@ -87,7 +87,7 @@ int linear(const char *fn, int bits, const void *x, const sx_qview *w, void *y, 
         SX_HIP(dks::launch(bits, w->G, act, out_act, d, device_cus(), stream_of(stream)), fn);
         return SX_OK;
     }
-    if (M >= gg::kDenseMinTokens && gg::eligible_dense(bits, w->G, w->K, act) && aligned(w->scale, 4) &&
+    if (M >= gg::dense_min_tokens(bits) && gg::eligible_dense(bits, w->G, w->K, act) && aligned(w->scale, 4) &&
         aligned(w->minv, 4)) {  // prefill width: the grouped kernel's MFMA tiles, the tokens as one bucket
         SX_HIP(gg::launch_dense(x, w, y, M, out_act, stream_of(stream)), fn);
         return SX_OK;

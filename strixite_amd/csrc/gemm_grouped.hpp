@@ -9,9 +9,11 @@ namespace sx::gg {
 constexpr int64_t kPrefillMinTokens = 32;
 
 bool eligible(int bits, int64_t G, int64_t K, int act);
-// Tokens from which a dense q4 linear takes the grouped kernel's tiles (launch_dense): below, its few tiles leave
-// the chip idle and qmm's dense mode is faster (4096 x 4096: 41 against 61 us at M = 128, 73 against 62 at 256).
-constexpr int64_t kDenseMinTokens = 256;
+// Tokens from which a dense linear takes the grouped kernel's tiles (launch_dense): below, its few tiles leave the
+// chip idle and qmm's dense mode is faster. 4096 x 4096, qmm against the tiles: q4 37 / 59 us at M = 128, 64 / 59 at
+// 255; q8 68 / 91 at 128, 88 / 92 at 192, 115 / 92 at 255.
+constexpr int64_t kDenseMinTokens = 256, kDenseMinTokensQ8 = 200;
+constexpr int64_t dense_min_tokens(int bits) { return bits == 8 ? kDenseMinTokensQ8 : kDenseMinTokens; }
 // The dense linears the tiles take: eligible's q4, and q8 (G = 64, K % 256 == 0, K <= 4096, BF16 x).
 bool eligible_dense(int bits, int64_t G, int64_t K, int act);
 // A dense linear at prefill width on the same tiles: y [M, w->N] (BF16 or FP32) = x [M, K] (BF16) . deq(w)^T, tile u

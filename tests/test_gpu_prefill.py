@@ -118,6 +118,7 @@ def test_config4_prefill_layer_full_size():
                                                      (8, 64, orc.BF16, orc.F32, 2048, 4096),
                                                      (8, 64, orc.BF16, orc.BF16, 300, 1280),
                                                      (8, 64, orc.BF16, orc.BF16, 256, 4352),
+                                                     (8, 64, orc.BF16, orc.F32, 200, 768),
                                                      (4, 128, orc.F32, orc.F32, 2048, 4096)])
 def test_dense_linear_prefill_width(bits, G, act, out_act, M, K):
     """linear_q4 / linear_q8 at prefill width (the route *_wmma callers take; q4 G = 128 and q8 G = 64 with BF16 x on
