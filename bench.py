@@ -40,6 +40,8 @@ def parse():
                     help="only config 4's prefill layer (for rocprofv3 runs): one JSON line with its timings")
     ap.add_argument("--draft-only", action="store_true",
                     help="only the MTP draft head (for rocprofv3 runs): one JSON line with its timings")
+    ap.add_argument("--dense-only", action="store_true",
+                    help="only the dense prefill-width linears (for rocprofv3 runs): one JSON line with their timings")
     ap.add_argument("--tail-only", action="store_true",
                     help="only config 5's verify tail (for rocprofv3 runs): one JSON line with its timings")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -361,26 +363,30 @@ def extra_configs(out):
                      "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del reps
     # config 4: the MoE layer at prefill width, M = 2048, Zipf-skewed routing; grouped MFMA experts
-    # a dense q4 linear at prefill width (the route linear_q4_wmma's callers take), 4096 x 4096 at M = 2048
-    w = syn.qweight(4, 4096, 4096, 128, seed=70)
-    x = syn.activations(2048, 4096, seed=71)
-    y = torch.empty((2048, 4096), dtype=torch.bfloat16, device="cuda")
-    ms = time_window(lambda i: kx.linear(x, w, y=y), min_launches=20, min_ms=20.0)
-    res["prefill_dense_q4_4096x4096_M2048"] = {"us": round(ms * 1e3, 1),
-                                               "mfma_frac": round(2.0 * 2048 * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
-    del w, x, y
-    # the same at q8 G = 64 (linear_q8_wmma's callers)
-    w = syn.qweight(8, 4096, 4096, 64, seed=72)
-    x = syn.activations(2048, 4096, seed=73)
-    y = torch.empty((2048, 4096), dtype=torch.bfloat16, device="cuda")
-    ms = time_window(lambda i: kx.linear(x, w, y=y), min_launches=20, min_ms=20.0)
-    res["prefill_dense_q8_4096x4096_M2048"] = {"us": round(ms * 1e3, 1),
-                                               "mfma_frac": round(2.0 * 2048 * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
-    del w, x, y
+    res.update(dense_prefill())
     res["cfg4_prefill_layer"] = prefill_layer()
     res["cfg5_verify_tail"] = verify_tail()
     res["mtp_draft_head"] = draft_head()
     out["configs"] = res
+
+
+def dense_prefill():
+    """Dense linears at prefill width (the route linear_q4_wmma / linear_q8_wmma's callers take): 4096 x 4096 at
+    M = 2048, q4 G = 128 and q8 G = 64, BF16 in and out."""
+    import torch
+
+    from strixite_amd import kernels as kx
+    from strixite_amd import synthetic as syn
+    res = {}
+    for bits, G, seed in ((4, 128, 70), (8, 64, 72)):
+        w = syn.qweight(bits, 4096, 4096, G, seed=seed)
+        x = syn.activations(2048, 4096, seed=seed + 1)
+        y = torch.empty((2048, 4096), dtype=torch.bfloat16, device="cuda")
+        ms = time_window(lambda i: kx.linear(x, w, y=y), min_launches=20, min_ms=20.0)
+        res[f"prefill_dense_q{bits}_4096x4096_M2048"] = {
+            "us": round(ms * 1e3, 1), "mfma_frac": round(2.0 * 2048 * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
+        del w, x, y
+    return res
 
 
 def verify_tail():
@@ -533,6 +539,9 @@ def main():
         return
     if args.tail_only:
         print(json.dumps({"cfg5_verify_tail": verify_tail()}))
+        return
+    if args.dense_only:
+        print(json.dumps(dense_prefill()))
         return
 
     out = {"metric": METRIC, "value": None, "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
