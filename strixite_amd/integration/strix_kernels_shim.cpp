@@ -2,7 +2,7 @@
 //
 // A maintainer adds this file to strixite's strix_kernels target in place of kernels/linear.hip, linear_q4.hip,
 // linear_q56.hip, linear_q8.hip, linear_wmma.hip, moe_router.hip, moe_grouped.hip, swiglu.hip, logits_topk.hip and
-// mtp_pick.hip (INTEGRATION.md), and links libstrixite_amd.so; it is
+// mtp_pick.hip, and links libstrixite_amd.so; it is
 // compiled inside the strixite tree (it includes strixite's own headers), so runtime/qwen4exp.cpp and serve/engine.cpp
 // call the gfx950 kernels without a change. Every function forwards to the sx_* entry point that replaces it and turns
 // a nonzero status into strix::Error with the library's message (common/check.hpp's exception type).

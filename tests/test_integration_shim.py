@@ -1,6 +1,6 @@
 """The drop-in boundary without a GPU: strixite_amd/integration/strix_kernels_shim.cpp defines, with identical
 signatures, every operator that the reference's kernels/*.hpp headers declare for the source files the integration
-recipe (INTEGRATION.md) removes from strix_kernels, and nothing else outside its anonymous namespace; and every C-ABI
+recipe removes from strix_kernels, and nothing else outside its anonymous namespace; and every C-ABI
 entry point it calls is declared in include/strixite_amd.h.
 
 The shim cannot be compiled here: strixite's common/hip_runtime.hpp includes <format>, which this GCC lacks. The
