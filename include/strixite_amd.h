@@ -158,8 +158,8 @@ int sx_linear_q4_experts_gather_swiglu_grouped(const void *x, const sx_qview *w,
 /* ---- SwiGLU, kernels/swiglu.hpp:21: gu [rows, 2I] -> h [rows, I]; BF16: h = bf16(bf16(silu(g)) * u). ---- */
 int sx_swiglu(const void *gu, void *h, int64_t rows, int64_t I, int act, sx_stream stream);
 
-/* ---- dense FP32-weight projection: y[M, N] (F32) = x[M, K] (act) * W[N, K]^T. The router logits of BASELINE
- * configs 3/4 (fp32 Wr); plays the role kernels/linear.hpp linear_bf16w plays at runtime/qwen4exp.cpp:1132-1137. ---- */
+/* ---- dense FP32-weight projection: y[M, N] (F32) = x[M, K] (act) * W[N, K]^T. The router logits of the
+ * benchmark's MoE layers (fp32 Wr); plays the role kernels/linear.hpp linear_bf16w plays at runtime/qwen4exp.cpp:1132-1137. ---- */
 int sx_linear_f32w(const void *x, const float *W, int64_t N, int64_t K, float *y, int64_t M, int act,
                    sx_stream stream);
 
