@@ -53,21 +53,14 @@ struct Tensor {
     std::vector<Component> comps;
 };
 
-// A format violation: the text names what is wrong; the C boundary prefixes the file unless `whole` (the message of a
-// record's shape / encoding check, which names the tensor alone, as the reference's does).
+// A file this reader refuses; the C boundary puts the function and the file's path in front of the text.
 struct Reject {
     std::string msg;
-    bool whole = false;
 };
 
 template <typename... Args>
 [[noreturn]] void reject(Args &&...args) {
     throw Reject{sx::cat(std::forward<Args>(args)...)};
-}
-
-template <typename... Args>
-[[noreturn]] void reject_record(Args &&...args) {
-    throw Reject{sx::cat("strixw tensor ", std::forward<Args>(args)...), true};
 }
 
 std::string shape_text(const std::vector<int64_t> &s) {
@@ -76,17 +69,33 @@ std::string shape_text(const std::vector<int64_t> &s) {
     return r + "]";
 }
 
-const char *encoding_name(uint8_t e) {
-    static const char *names[] = {"?", "q4", "q4-chunk-major", "bf16", "f32", "i64", "q8", "q8-chunk-major", "q6", "q5"};
-    return e >= 1 && e <= 9 ? names[e] : "unknown";
-}
+// The encodings the format defines (formats/strixw.hpp), by their code in the index. A grouped encoding stores
+// `bits` code bits a weight (rows of K codes, K a multiple of `k_multiple`), then BF16 scale and min [N, K/G]; a plain
+// one stores `elem_bytes` a value in one data component.
+struct Encoding {
+    const char *name;
+    int bits;           // grouped: code bits a weight; 0 for a plain encoding
+    int k_multiple;     // grouped: K must be a multiple of this (the packing of 6- and 5-bit codes)
+    int elem_bytes;     // plain: bytes a value
+};
+constexpr Encoding kEncodings[] = {
+    {nullptr, 0, 0, 0},       {"q4", 4, 1, 0},   {"q4-chunk-major", 4, 1, 0}, {"bf16", 0, 0, 2},
+    {"f32", 0, 0, 4},         {"i64", 0, 0, 8},  {"q8", 8, 1, 0},             {"q8-chunk-major", 8, 1, 0},
+    {"q6", 6, 64, 0},         {"q5", 5, 128, 0},
+};
+constexpr int kEncodingCount = (int)(sizeof(kEncodings) / sizeof(kEncodings[0]));
 
+const Encoding *encoding_of(uint8_t code) {
+    return code >= 1 && code < kEncodingCount ? &kEncodings[code] : nullptr;
+}
+const char *encoding_name(uint8_t code) {
+    const Encoding *e = encoding_of(code);
+    return e ? e->name : "unknown";
+}
 const char *role_name(uint8_t r) {
     static const char *names[] = {"data", "q", "scale", "min"};
     return r <= 3 ? names[r] : "unknown";
 }
-
-uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
 // strix_hash64 (formats/strixw.cpp:253-274): the file's own 64-bit checksum, so it is computed exactly as the
 // writer computes it. Four multiply-xorshift lanes take the 32-byte blocks; the 8-byte words after the last block go
@@ -123,80 +132,227 @@ uint64_t hash64(const uint8_t *p, uint64_t n) {
     return r ^ (r >> 29);
 }
 
-// The components an encoding has and their sizes for a record's shape and group (formats/strixw.cpp:177-251):
-// q4 / q8 / q6 / q5 (row- or chunk-major) [N, K] with G in {32, 64, 128} dividing K: codes (N*K/2, N*K, N*3K/4 with
-// K % 64 == 0, N*5K/8 with K % 128 == 0), then BF16 scale and min [N, K/G]; bf16 / f32 / i64 (group 0): one data
-// component of numel * 2 / 4 / 8 bytes.
-std::vector<Component> expected_components(const Tensor &t) {
-    int64_t numel = 1;
-    for (int64_t d : t.shape) {
-        if (d < 1 || numel > INT64_MAX / d) reject_record("'", t.name, "': bad shape ", shape_text(t.shape));
-        numel *= d;
-    }
-    auto make = [](uint8_t role, int64_t bytes) { return Component{role, 0, (uint64_t)bytes, 0}; };
-    const uint8_t e = t.encoding;
-    if (e == 1 || e == 2 || e == 6 || e == 7 || e == 8 || e == 9) {
-        if (t.shape.size() != 2)
-            reject_record("'", t.name, "': ", encoding_name(e), " needs shape [N, K], got ", shape_text(t.shape));
-        const int64_t N = t.shape[0], K = t.shape[1], G = t.group;
-        const int64_t kmul = e == 8 ? 64 : e == 9 ? 128 : 1;
-        if (!(G == 32 || G == 64 || G == 128) || K % G != 0 || K % kmul != 0)
-            reject_record("'", t.name, "': ", encoding_name(e), " with K = ", K, ", group size ", G,
-                   " (must be 32/64/128 and divide K", kmul > 1 ? "; K a multiple of " + std::to_string(kmul) : "",
-                   ")");
-        const int64_t code_bytes = e == 1 || e == 2 ? N * K / 2 : e == 6 || e == 7 ? N * K
-                                   : e == 8 ? N * (K / 2 + K / 4) : N * (K / 2 + K / 8);
-        const int64_t side = N * (K / G) * 2;
-        return {make(1, code_bytes), make(2, side), make(3, side)};
-    }
-    if (e == 3 || e == 4 || e == 5) {
-        if (t.group != 0) reject_record("'", t.name, "': ", encoding_name(e), " has group size ", t.group, ", expected 0");
-        const int64_t es = e == 3 ? 2 : e == 4 ? 4 : 8;
-        if (numel > INT64_MAX / es) reject_record("'", t.name, "': ", numel, " elements overflow");
-        return {make(0, numel * es)};
-    }
-    reject_record("'", t.name, "': unknown encoding ", (int)e);
+// ---- the header: decoded whole, then judged by a list of rules taken in order ----
+
+struct Header {
+    char magic[8];
+    uint32_t version, header_bytes;
+    uint64_t index_offset, index_bytes, data_offset, file_bytes, index_hash, header_hash;
+};
+
+Header decode_header(const uint8_t *b) {
+    Header h;
+    std::memcpy(h.magic, b, 8);
+    std::memcpy(&h.version, b + 8, 4);
+    std::memcpy(&h.header_bytes, b + 12, 4);
+    std::memcpy(&h.index_offset, b + 16, 8);
+    std::memcpy(&h.index_bytes, b + 24, 8);
+    std::memcpy(&h.data_offset, b + 32, 8);
+    std::memcpy(&h.file_bytes, b + 40, 8);
+    std::memcpy(&h.index_hash, b + 48, 8);
+    std::memcpy(&h.header_hash, b + 120, 8);
+    return h;
 }
 
-// What every record must satisfy apart from its components (formats/strixw.cpp:80-100).
-void check_record(const Tensor &t) {
-    if (t.name.empty()) reject("tensor with an empty name");
-    if (t.shape.empty() || t.shape.size() > 8)
-        reject("tensor '", t.name, "' has ", t.shape.size(), " dims, expected 1..8");
-    for (int64_t d : t.shape)
-        if (d < 1) reject("tensor '", t.name, "' has shape ", shape_text(t.shape));
-    if (t.experts < 0 || (t.experts > 0 && t.shape[0] % t.experts != 0))
-        reject("tensor '", t.name, "': ", t.shape[0], " rows don't split into ", t.experts, " experts");
-    int64_t row = 0;
-    for (const Part &p : t.parts) {
-        if (p.source.empty() || p.rows < 1 || p.row_offset != row)
-            reject("tensor '", t.name, "' part '", p.source, "' at row ", p.row_offset, " (", p.rows,
-                   " rows), expected to start at row ", row);
-        row += p.rows;
-    }
-    if (!t.parts.empty() && row != t.shape[0])
-        reject("tensor '", t.name, "' parts cover ", row, " rows of ", t.shape[0]);
-}
+// Each rule sees the header, the mapping and its size, and returns an empty string when the file passes it. The
+// order matters only for which complaint a doubly broken file gets: the checksums come after the fields that say
+// where the bytes they cover are.
+using HeaderRule = std::string (*)(const Header &, const uint8_t *, uint64_t);
 
-// Little-endian reads off the index, each bounds-checked against the index's end.
-struct IndexReader {
-    const uint8_t *p;
-    uint64_t n, at = 0;
+const HeaderRule kHeaderRules[] = {
+    [](const Header &h, const uint8_t *, uint64_t) -> std::string {
+        return std::memcmp(h.magic, "STRIXWT", 8) == 0 ? "" : "no STRIXWT signature at byte 0";
+    },
+    [](const Header &h, const uint8_t *, uint64_t) -> std::string {
+        if (h.version >= kOldestVersion && h.version <= kNewestVersion) return "";
+        return sx::cat("written as version ", h.version, "; versions ", kOldestVersion, " to ", kNewestVersion,
+                       " are readable (convert the weights again)");
+    },
+    [](const Header &h, const uint8_t *, uint64_t) -> std::string {
+        return h.header_bytes == kHeaderBytes ? "" : sx::cat("declares a ", h.header_bytes, "-byte header, not ", kHeaderBytes);
+    },
+    [](const Header &h, const uint8_t *b, uint64_t) -> std::string {
+        return h.header_hash == hash64(b, 120) ? "" : "checksum of header bytes 0..119 does not match";
+    },
+    [](const Header &h, const uint8_t *, uint64_t size) -> std::string {
+        return h.file_bytes == size ? "" : sx::cat("length on disk ", size, " differs from the recorded ", h.file_bytes);
+    },
+    [](const Header &h, const uint8_t *, uint64_t size) -> std::string {
+        if (h.index_offset == kHeaderBytes && h.index_bytes <= size - h.index_offset) return "";
+        return sx::cat("index [", h.index_offset, ", +", h.index_bytes, ") is not right after the header inside ", size,
+                       " bytes");
+    },
+    [](const Header &h, const uint8_t *, uint64_t size) -> std::string {
+        const uint64_t index_end = h.index_offset + h.index_bytes;
+        if (h.data_offset % kTensorAlign == 0 && h.data_offset >= index_end && h.data_offset <= size) return "";
+        return sx::cat("data region start ", h.data_offset, " must be a multiple of ", kTensorAlign, " in [", index_end,
+                       ", ", size, "]");
+    },
+    [](const Header &h, const uint8_t *b, uint64_t) -> std::string {
+        return h.index_hash == hash64(b + h.index_offset, h.index_bytes) ? "" : "checksum of the index does not match";
+    },
+};
+
+// ---- the index: a stream with a sticky failure, decoded in one pass ----
+
+// Reads little-endian fields off the index. A read past the end leaves the target zeroed and marks the stream
+// broken; the decoder checks once a record, and the first field that did not fit names the place.
+class IndexStream {
+public:
+    IndexStream(const uint8_t *p, uint64_t n) : p_(p), n_(n) {}
+
     template <typename T>
-    T get(const char *what) {
-        if (n - at < sizeof(T)) reject("index ends inside ", what, " (at index byte ", at, " of ", n, ")");
-        T v;
-        std::memcpy(&v, p + at, sizeof(T));
-        at += sizeof(T);
+    T next(const char *field) {
+        T v{};
+        if (take(sizeof(T), field)) std::memcpy(&v, p_ + pos_ - sizeof(T), sizeof(T));
         return v;
     }
-    std::string text(uint64_t len, const char *what) {
-        if (n - at < len) reject("index ends inside ", what, " (", len, " bytes at index byte ", at, " of ", n, ")");
-        std::string s(reinterpret_cast<const char *>(p + at), len);
-        at += len;
-        return s;
+    template <typename LenT>
+    std::string next_text(const char *field) {
+        const uint64_t len = next<LenT>(field);
+        if (!take(len, field)) return {};
+        return std::string(reinterpret_cast<const char *>(p_ + pos_ - len), len);
     }
+    void require_intact(const char *record) const {
+        if (short_field_)
+            reject("the index (", n_, " bytes) stops short of the ", short_field_, " of ", record);
+    }
+    uint64_t left() const { return n_ - pos_; }
+
+private:
+    bool take(uint64_t len, const char *field) {
+        if (short_field_) return false;
+        if (n_ - pos_ < len) {
+            short_field_ = field;
+            return false;
+        }
+        pos_ += len;
+        return true;
+    }
+    const uint8_t *p_;
+    uint64_t n_, pos_ = 0;
+    const char *short_field_ = nullptr;
 };
+
+Tensor decode_record(IndexStream &in) {
+    Tensor t;
+    t.name = in.next_text<uint16_t>("name");
+    t.encoding = in.next<uint8_t>("encoding");
+    const uint8_t ndim = in.next<uint8_t>("rank");
+    for (uint8_t d = 0; d < ndim; ++d) t.shape.push_back(in.next<int64_t>("dimension"));
+    t.group = in.next<int64_t>("group size");
+    t.experts = in.next<int64_t>("expert count");
+    const uint16_t nparts = in.next<uint16_t>("part count");
+    for (uint16_t i = 0; i < nparts; ++i) {
+        Part part;
+        part.source = in.next_text<uint16_t>("part source");
+        part.row_offset = in.next<int64_t>("part first row");
+        part.rows = in.next<int64_t>("part row count");
+        t.parts.push_back(std::move(part));
+    }
+    const uint8_t ncomp = in.next<uint8_t>("component count");
+    for (uint8_t i = 0; i < ncomp; ++i) {
+        Component c;
+        c.role = in.next<uint8_t>("component role");
+        c.offset = in.next<uint64_t>("component offset");
+        c.bytes = in.next<uint64_t>("component size");
+        c.hash = in.next<uint64_t>("component checksum");
+        t.comps.push_back(c);
+    }
+    return t;
+}
+
+// ---- a record's rules: geometry, row partition, then the components the encoding implies and where they lie ----
+
+// The (role, bytes) list an encoding implies for the record's shape and group size, or a reason it cannot hold it.
+bool implied_components(const Tensor &t, std::vector<std::pair<uint8_t, uint64_t>> &out, std::string &why) {
+    const Encoding *e = encoding_of(t.encoding);
+    if (!e) {
+        why = sx::cat("encoding code ", (int)t.encoding, " is not one this format defines");
+        return false;
+    }
+    uint64_t numel = 1;
+    for (int64_t d : t.shape) {
+        if ((uint64_t)d > (uint64_t)INT64_MAX / numel) {
+            why = sx::cat("shape ", shape_text(t.shape), " holds more than 2^63 values");
+            return false;
+        }
+        numel *= (uint64_t)d;
+    }
+    if (e->bits == 0) {
+        if (t.group != 0) {
+            why = sx::cat(e->name, " values take no group size (found ", t.group, ")");
+            return false;
+        }
+        if (numel > (uint64_t)INT64_MAX / (uint64_t)e->elem_bytes) {
+            why = sx::cat(numel, " ", e->name, " values exceed the addressable size");
+            return false;
+        }
+        out = {{0, numel * (uint64_t)e->elem_bytes}};
+        return true;
+    }
+    if (t.shape.size() != 2) {
+        why = sx::cat(e->name, " is a matrix encoding; shape ", shape_text(t.shape), " is not [rows, K]");
+        return false;
+    }
+    const uint64_t N = (uint64_t)t.shape[0], K = (uint64_t)t.shape[1];
+    const bool group_ok = t.group == 32 || t.group == 64 || t.group == 128;
+    if (!group_ok || K % (uint64_t)t.group != 0 || K % (uint64_t)e->k_multiple != 0) {
+        why = sx::cat(e->name, " needs a group size of 32, 64 or 128 dividing K",
+                      e->k_multiple > 1 ? sx::cat(" and K divisible by ", e->k_multiple) : std::string(), "; K = ", K,
+                      ", group size ", t.group);
+        return false;
+    }
+    const uint64_t side = N * (K / (uint64_t)t.group) * 2;
+    out = {{1, N * K * (uint64_t)e->bits / 8}, {2, side}, {3, side}};
+    return true;
+}
+
+// Every rule a single record must meet on its own; `data_offset` and `size` bound where its components may lie.
+void validate_record(const Tensor &t, uint64_t data_offset, uint64_t size) {
+    const std::string who = t.name.empty() ? std::string("an unnamed tensor") : sx::cat("tensor '", t.name, "'");
+    if (t.name.empty()) reject("the index holds ", who);
+    if (t.shape.empty() || t.shape.size() > 8) reject(who, ": rank ", t.shape.size(), " is outside 1..8");
+    if (std::any_of(t.shape.begin(), t.shape.end(), [](int64_t d) { return d < 1; }))
+        reject(who, ": every dimension must be positive, shape is ", shape_text(t.shape));
+    if (t.experts < 0) reject(who, ": negative expert count ", t.experts);
+    if (t.experts > 0 && t.shape[0] % t.experts != 0)
+        reject(who, ": ", t.experts, " experts cannot share ", t.shape[0], " rows evenly");
+
+    // The parts tile the rows in order, with no gap and no overlap.
+    int64_t next_row = 0;
+    for (size_t i = 0; i < t.parts.size(); ++i) {
+        const Part &p = t.parts[i];
+        if (p.source.empty()) reject(who, ": part ", i, " has no source name");
+        if (p.rows < 1 || p.row_offset != next_row)
+            reject(who, ": part ", i, " ('", p.source, "') covers rows from ", p.row_offset, " (", p.rows,
+                   " of them) where row ", next_row, " comes next");
+        next_row += p.rows;
+    }
+    if (!t.parts.empty() && next_row != t.shape[0])
+        reject(who, ": its parts end at row ", next_row, " of ", t.shape[0]);
+
+    std::vector<std::pair<uint8_t, uint64_t>> implied;
+    std::string why;
+    if (!implied_components(t, implied, why)) reject(who, ": ", why);
+    if (implied.size() != t.comps.size())
+        reject(who, ": ", encoding_name(t.encoding), " stores ", implied.size(), " components, the index lists ",
+               t.comps.size());
+    for (size_t i = 0; i < implied.size(); ++i) {
+        const Component &c = t.comps[i];
+        if (c.role != implied[i].first || c.bytes != implied[i].second)
+            reject(who, ": listed component ", i, " (", role_name(c.role), ", ", c.bytes, " bytes) should be ",
+                   role_name(implied[i].first), ", ", implied[i].second, " bytes for ", encoding_name(t.encoding), " ",
+                   shape_text(t.shape));
+        if (c.offset % kComponentAlign != 0)
+            reject(who, ": ", role_name(c.role), " starts at ", c.offset, ", not on a ", kComponentAlign,
+                   "-byte boundary");
+        // (offset > size first: size - offset would wrap for a component placed past the end of the file)
+        if (c.offset < data_offset || c.offset > size || c.bytes > size - c.offset)
+            reject(who, ": ", role_name(c.role), " bytes [", c.offset, ", +", c.bytes, ") fall outside the data region [",
+                   data_offset, ", ", size, ")");
+    }
+}
 
 }  // namespace
 
@@ -214,87 +370,51 @@ struct sx_strixw {
         if (map) ::munmap(const_cast<uint8_t *>(map), size);
     }
 
+    // The header's rules, then the index in one pass (metadata, then each record decoded and validated), then the
+    // file-wide rules: unique names, nothing left over, no two components sharing a byte.
     void parse() {
-        const uint8_t *b = map;
-        auto u32 = [&](uint64_t off) { uint32_t v; std::memcpy(&v, b + off, 4); return v; };
-        auto u64 = [&](uint64_t off) { uint64_t v; std::memcpy(&v, b + off, 8); return v; };
-        if (std::memcmp(b, "STRIXWT", 8) != 0) reject("not a strixw file (bad magic)");
-        version = u32(8);
-        if (version < kOldestVersion || version > kNewestVersion)
-            reject("format version ", version, ", this build reads ", kOldestVersion, "..", kNewestVersion,
-                   " (re-run the converter)");
-        if (u32(12) != kHeaderBytes) reject("header size ", u32(12), ", expected ", kHeaderBytes);
-        if (u64(120) != hash64(b, 120)) reject("header hash mismatch (corrupt header)");
-        const uint64_t index_off = u64(16), index_bytes = u64(24), file_bytes = u64(40);
-        data_offset = u64(32);
-        if (file_bytes != size) reject("header says ", file_bytes, " bytes, the file has ", size, " (truncated or appended to)");
-        if (index_off != kHeaderBytes || index_bytes > size - index_off)
-            reject("index at ", index_off, " (", index_bytes, " bytes) doesn't fit the ", size, "-byte file");
-        if (data_offset % kTensorAlign != 0 || data_offset < index_off + index_bytes || data_offset > size)
-            reject("data offset ", data_offset, " (index ends at ", index_off + index_bytes, ", alignment ", kTensorAlign,
-                   ")");
-        if (u64(48) != hash64(b + index_off, index_bytes)) reject("index hash mismatch (corrupt index)");
-
-        IndexReader r{b + index_off, index_bytes};
-        const uint32_t nmeta = r.get<uint32_t>("metadata count");
-        for (uint32_t i = 0; i < nmeta; ++i) {
-            std::string key = r.text(r.get<uint16_t>("metadata key length"), "metadata key");
-            std::string val = r.text(r.get<uint32_t>("metadata value length"), "metadata value");
-            if (!meta_at.emplace(key, meta.size()).second) reject("metadata key '", key, "' twice");
-            meta.emplace_back(std::move(key), std::move(val));
+        const Header h = decode_header(map);
+        for (HeaderRule rule : kHeaderRules) {
+            const std::string problem = rule(h, map, size);
+            if (!problem.empty()) reject(problem);
         }
-        const uint32_t ntensors = r.get<uint32_t>("tensor count");
-        if (ntensors < 1) reject("no tensors");
-        std::vector<std::pair<uint64_t, uint64_t>> spans;
+        version = h.version;
+        data_offset = h.data_offset;
+
+        IndexStream in(map + h.index_offset, h.index_bytes);
+        const uint32_t nmeta = in.next<uint32_t>("entry count");
+        in.require_intact("the metadata");
+        for (uint32_t i = 0; i < nmeta; ++i) {
+            std::string key = in.next_text<uint16_t>("key");
+            std::string value = in.next_text<uint32_t>("value");
+            in.require_intact(sx::cat("metadata entry ", i).c_str());
+            if (meta_at.count(key)) reject("metadata key '", key, "' appears more than once");
+            meta_at[key] = meta.size();
+            meta.emplace_back(std::move(key), std::move(value));
+        }
+        const uint32_t ntensors = in.next<uint32_t>("tensor count");
+        in.require_intact("the tensor list");
+        if (ntensors == 0) reject("the index lists no tensors");
+
+        struct Extent {
+            uint64_t begin, end;
+            bool operator<(const Extent &o) const { return begin < o.begin; }
+        };
+        std::vector<Extent> extents;
         for (uint32_t i = 0; i < ntensors; ++i) {
-            Tensor t;
-            t.name = r.text(r.get<uint16_t>("tensor name length"), "tensor name");
-            t.encoding = r.get<uint8_t>("encoding");
-            const uint8_t ndim = r.get<uint8_t>("ndim");
-            for (uint8_t d = 0; d < ndim; ++d) t.shape.push_back(r.get<int64_t>("shape"));
-            t.group = r.get<int64_t>("group size");
-            t.experts = r.get<int64_t>("experts");
-            const uint16_t nparts = r.get<uint16_t>("part count");
-            for (uint16_t p = 0; p < nparts; ++p) {
-                Part part;
-                part.source = r.text(r.get<uint16_t>("part name length"), "part name");
-                part.row_offset = r.get<int64_t>("part row offset");
-                part.rows = r.get<int64_t>("part rows");
-                t.parts.push_back(std::move(part));
-            }
-            const uint8_t ncomp = r.get<uint8_t>("component count");
-            for (uint8_t c = 0; c < ncomp; ++c) {
-                Component comp;
-                comp.role = r.get<uint8_t>("component role");
-                comp.offset = r.get<uint64_t>("component offset");
-                comp.bytes = r.get<uint64_t>("component bytes");
-                comp.hash = r.get<uint64_t>("component hash");
-                t.comps.push_back(comp);
-            }
-            check_record(t);
-            const std::vector<Component> want = expected_components(t);
-            if (want.size() != t.comps.size())
-                reject("tensor '", t.name, "' (", encoding_name(t.encoding), ") has ", t.comps.size(),
-                       " components, expected ", want.size());
-            for (size_t c = 0; c < want.size(); ++c) {
-                const Component &g = t.comps[c];
-                if (g.role != want[c].role || g.bytes != want[c].bytes)
-                    reject("tensor '", t.name, "' component ", c, " is ", role_name(g.role), " of ", g.bytes,
-                           " bytes, expected ", role_name(want[c].role), " of ", want[c].bytes, " for ",
-                           encoding_name(t.encoding), " ", shape_text(t.shape));
-                if (g.offset < data_offset || g.offset % kComponentAlign != 0 || g.bytes > size - g.offset)
-                    reject("tensor '", t.name, "' ", role_name(g.role), " at ", g.offset, " (", g.bytes,
-                           " bytes) is outside the data region [", data_offset, ", ", size, ") or not ",
-                           kComponentAlign, "-aligned");
-                spans.emplace_back(g.offset, g.offset + g.bytes);
-            }
-            if (!tensor_at.emplace(t.name, tensors.size()).second) reject("tensor '", t.name, "' twice");
+            Tensor t = decode_record(in);
+            in.require_intact(sx::cat("tensor record ", i).c_str());
+            validate_record(t, data_offset, size);
+            if (tensor_at.count(t.name)) reject("tensor '", t.name, "' is listed more than once");
+            for (const Component &c : t.comps) extents.push_back({c.offset, c.offset + c.bytes});
+            tensor_at[t.name] = tensors.size();
             tensors.push_back(std::move(t));
         }
-        if (r.at != r.n) reject(r.n - r.at, " unread bytes after the last index record");
-        std::sort(spans.begin(), spans.end());
-        for (size_t i = 1; i < spans.size(); ++i)
-            if (spans[i].first < spans[i - 1].second) reject("components overlap at byte ", spans[i].first);
+        if (in.left() != 0) reject("the index has ", in.left(), " bytes past its last tensor record");
+        std::sort(extents.begin(), extents.end());
+        for (size_t i = 1; i < extents.size(); ++i)
+            if (extents[i].begin < extents[i - 1].end)
+                reject("two components share bytes from ", extents[i].begin);
     }
 };
 
@@ -306,7 +426,7 @@ int guarded(const char *fn_name, const std::string &where, Fn &&fn) {
     try {
         return fn();
     } catch (const Reject &r) {
-        sx::set_error(r.whole ? sx::cat(fn_name, ": ", r.msg) : sx::cat(fn_name, ": ", where, ": ", r.msg));
+        sx::set_error(sx::cat(fn_name, ": ", where, ": ", r.msg));
         return SX_EINVAL;
     } catch (const std::exception &e) {
         sx::set_error(sx::cat(fn_name, ": ", where, ": ", e.what()));
@@ -431,7 +551,7 @@ int sx_strixw_open(const char *path, sx_strixw **out) {
         f->size = (uint64_t)st.st_size;
         if (f->size < kHeaderBytes) {
             ::close(fd);
-            reject(f->size, " bytes, smaller than the ", kHeaderBytes, "-byte header");
+            reject("only ", f->size, " bytes: too short for the ", kHeaderBytes, "-byte header");
         }
         void *m = ::mmap(nullptr, f->size, PROT_READ, MAP_PRIVATE, fd, 0);
         const int e = errno;
@@ -550,7 +670,7 @@ int sx_strixw_load(const sx_strixw *f, void *dst, uint64_t dst_bytes, int read_t
     const hipStream_t s = sx::stream_of(stream);
     const int fd = ::open(f->path.c_str(), O_RDONLY | O_CLOEXEC);
     SX_CHECK(fd >= 0, "open '", f->path, "' failed: ", std::strerror(errno));
-    const uint64_t slot_bytes = std::min(kSlotBytes, round_up(n, kTensorAlign));
+    const uint64_t slot_bytes = std::min(kSlotBytes, (n + kTensorAlign - 1) / kTensorAlign * kTensorAlign);
     const uint64_t nchunks = (n + slot_bytes - 1) / slot_bytes;
     const int slots = (int)std::min<uint64_t>(kSlots, nchunks);
     void *stage[kSlots] = {};
