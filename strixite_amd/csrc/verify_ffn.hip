@@ -1062,14 +1062,23 @@ int check_down(const char *fn, int64_t M, int64_t A, int64_t Ew, const sx_qview 
 
 std::atomic<uint64_t *> g_layer_trace{nullptr};
 
-// The launch number of a sync buffer: 1, 2, ... (never 0, the value of a freshly zeroed buffer).
-uint32_t next_epoch(const void *sync) {
-    static std::mutex mu;
-    static std::unordered_map<const void *, uint32_t> epochs;
-    std::lock_guard<std::mutex> lock(mu);
-    uint32_t &e = epochs[sync];
-    if (++e == 0) ++e;
-    return e;
+// The launch numbers of the sync buffers: 1, 2, ... (never 0, the value of a freshly zeroed buffer). A launch that
+// uses a buffer's pool takes the counter set of its number's parity and zeroes the other set for the next one, so the
+// numbers of the launches that use a buffer must alternate in parity: a number is reserved before the launch and
+// committed only once the launch went out (a failed launch, or one that does not use the pool, leaves it unused), and
+// the wrap goes from 0xFFFFFFFF (odd) to 2, skipping 0.
+std::mutex g_epoch_mu;
+std::unordered_map<const void *, uint32_t> g_epochs;
+
+uint32_t reserve_epoch(const void *sync) {
+    std::lock_guard<std::mutex> lock(g_epoch_mu);
+    const uint32_t last = g_epochs[sync];
+    return last == 0xFFFFFFFFu ? 2u : last + 1;
+}
+
+void commit_epoch(const void *sync, uint32_t e) {
+    std::lock_guard<std::mutex> lock(g_epoch_mu);
+    g_epochs[sync] = e;
 }
 
 }  // namespace
@@ -1107,12 +1116,15 @@ int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t
     p.logits = logits, p.ld = ld, p.shared_logit = shared_logit, p.shared_ld = shared_ld, p.shared_id = shared_id;
     p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = w->N / Ew, p.K = w->K;
     p.ids = ids, p.coef = coef, p.h = static_cast<uint16_t *>(h), p.h_sums = h_sums, p.router_err = router_err, p.expert_err = expert_err;
-    if (sync != nullptr) {
+    // The pool schedule exists for K = 4096 (eight K slices a block); other shapes split the items statically and
+    // leave the buffer untouched.
+    if (sync != nullptr && w->K == 4096) {
         SX_CHECK(aligned(sync, 16), fn, " sync must be 16-byte aligned");
         p.sync = static_cast<vf::LayerSync *>(sync);
-        p.epoch = next_epoch(sync);
+        p.epoch = reserve_epoch(sync);
     }
     SX_HIP(vf::launch_gate_up(p, device_cus(), stream_of(stream)), fn);
+    if (p.sync) commit_epoch(sync, p.epoch);
     return SX_OK;
 }
 
@@ -1185,8 +1197,9 @@ int sx_moe_verify_layer(const void *x, int64_t M, const void *wr, int wr_act, in
     lp.wr = wr, lp.rows = (int)rows, lp.logits = logits, lp.ld = rows, lp.sync = static_cast<vf::LayerSync *>(sync);
     lp.trace = g_layer_trace.load();
     lp.tagged = lp.sync->tagged;
-    lp.epoch = next_epoch(sync);
+    lp.epoch = reserve_epoch(sync);
     SX_HIP(vf::launch_layer(lp, wr_act == SX_ACT_F32, device_cus(), stream_of(stream)), fn);
+    commit_epoch(sync, lp.epoch);
     return SX_OK;
 }
 

@@ -122,6 +122,8 @@ void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t 
 }
 
 // ---- kernels/linear_wmma.hpp: the prefill-width dense linears run the same MFMA kernels (16 rows a weight pass) ----
+// With FP32 x these keep x exact (three BF16 planes on the matrix cores), where the reference's wmma contract rounds
+// x to BF16 first: the results are the exact path's, within FP32 rounding of the exact product.
 void linear_q4_wmma(const void *x, const Q4DeviceView &w, void *y, int64_t M, Act act, Act out_act,
                     hipStream_t stream) {
     linear_q4(x, w, y, M, act, out_act, stream);

@@ -34,7 +34,16 @@ class MoeVerifyLayer:
         self.partial = torch.empty((M * A, self.d), dtype=torch.float32, device=dev)
         self.y = torch.empty((M, self.d), dtype=act_dtype, device=dev)
         self.fused = fused and act_dtype == torch.bfloat16
-        self.sync = kx.verify_layer_sync(dev) if self.fused else None  # one per stream: forwards run in stream order
+        # the gate_up pool's sync buffers, one per stream: launches on one buffer must run in order, which only one
+        # stream guarantees
+        self._syncs = {}
+        self._dev = dev
+
+    def _sync_for(self, stream):
+        key = (stream or torch.cuda.current_stream(self._dev)).cuda_stream
+        if key not in self._syncs:
+            self._syncs[key] = kx.verify_layer_sync(self._dev)
+        return self._syncs[key]
 
     def _fused(self, M):
         return self.fused and kx.verify_supported(M, self.k, self.E, self.k, self.E, self.gate_up, self.down)
@@ -47,7 +56,7 @@ class MoeVerifyLayer:
         if self._fused(M):
             kx.verify_gate_up(x, self.logits[:M], self.gate_up, self.E, self.k, ids=self.ids[:M], coef=self.coef[:M],
                               h=self.h[:M], router_err=self.router_err, expert_err=self.expert_err,
-                              h_sums=self.h_sums, sync=self.sync, stream=stream)
+                              h_sums=self.h_sums, sync=self._sync_for(stream), stream=stream)
             kx.verify_down(self.h[:M], self.down, self.ids[:M], self.coef[:M], self.E, y=self.y[:M],
                            expert_err=self.expert_err, h_sums=self.h_sums, stream=stream)
             return self.y[:M]

@@ -135,3 +135,22 @@ def test_dense_linear_prefill_width(bits, G, act, out_act, M, K):
     sync()
     ref = orc.linear_q(x, w, out_act=out_act)
     util.assert_close(util.host_bits(y), ref, what=f"dense q{bits} M={M}")
+
+
+def test_f32_x_prefill_keeps_full_precision():
+    """The *_wmma entry points of the integration shim forward to linear_q4 / linear_q8, which keep FP32 x exact (three
+    BF16 planes) at every width; the reference's wmma contract rounds x to BF16 first (kernels/linear_wmma.hpp:3-6).
+    This pins the choice: the result is within FP32 rounding of the exact-x oracle and measurably apart from the
+    oracle on BF16-rounded x."""
+    M, N, K = 512, 256, 2048
+    rng = np.random.default_rng(77)
+    w = util.rand_qweight(rng, 4, N, K, 128)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    y = kx().linear(util.f32_dev(x), kx().QWeight.upload(w), out_act=orc.F32)
+    sync()
+    got = util.host_bits(y)
+    exact = orc.linear_q(x, w, out_act=orc.F32)
+    rounded = orc.linear_q(util.bf16_to_f32(util.f32_to_bf16(x)), w, out_act=orc.F32)
+    e_exact, e_round = util.max_abs_norm_err(got, exact), util.max_abs_norm_err(got, rounded)
+    print(f"F32 x: error vs exact x {e_exact:.3g}, vs BF16-rounded x {e_round:.3g}", flush=True)
+    assert e_exact < 1e-5 and e_round > 20 * e_exact

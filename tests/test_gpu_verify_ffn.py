@@ -180,3 +180,26 @@ def test_verify_gate_up_pool_matches_static_split(M, E, k, shared):
             outs.append((ids.cpu().numpy(), coef.cpu().numpy(), util.host_bits(h), hs.cpu().numpy()))
         for a, b, name in zip(outs[0], outs[1], ("ids", "coef", "h", "h_sums")):
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name} differs with the pool"
+
+
+def test_verify_gate_up_pool_survives_other_shapes_on_one_buffer():
+    """Launches that do not use the pool (K = 1024 gate_up with the same sync buffer) between K = 4096 launches that
+    do: the pool launches keep alternating counter sets, so each gives the static split's bits."""
+    import torch
+    from strixite_amd import synthetic as syn
+    M, E, k, I = 6, 64, 8, 512
+    sy = kx().verify_layer_sync()
+    g4 = syn.qweight(4, E * 2 * I, 4096, 128, seed=83)
+    g1 = syn.qweight(4, E * 2 * I, 1024, 128, seed=84)
+    for r, K in enumerate((4096, 1024, 4096, 1024, 1024, 4096, 4096, 1024, 4096)):
+        print(f"alternate: launch {r} K={K}", flush=True)
+        gu = g4 if K == 4096 else g1
+        x = syn.activations(M, K, seed=200 + r)
+        L = torch.randn((M, E), device="cuda") * 1.5
+        outs = []
+        for s in (None, sy):
+            ids, coef, h, rerr, eerr = kx().verify_gate_up(x, L, gu, E, k, Ew=E, sync=s)
+            sync()
+            assert list(eerr.cpu().numpy()[:3]) == [0, 0, 0]
+            outs.append((ids.cpu().numpy(), util.host_bits(h)))
+        assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1]), f"launch {r}"

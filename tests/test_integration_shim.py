@@ -3,11 +3,15 @@ signatures, every operator that the reference's kernels/*.hpp headers declare fo
 recipe removes from strix_kernels, and nothing else outside its anonymous namespace; and every C-ABI
 entry point it calls is declared in include/strixite_amd.h.
 
-The shim cannot be compiled here: strixite's common/hip_runtime.hpp includes <format>, which this GCC lacks. The
-check is therefore a comparison of the parsed declarations (types and order of the parameters, return type, default
-arguments left out). Skipped when the reference tree is absent (the GPU box)."""
+Two checks: a comparison of the parsed declarations (types and order of the parameters, return type, default
+arguments left out), and a compile of the shim against the reference's own headers with hipcc -fsyntax-only.
+strixite's common/hip_runtime.hpp includes <format>, which this image's GCC 11 lacks and which none of the headers the
+shim reaches uses, so the compile puts a directory holding an empty `format` header first on the include path.
+Skipped when the reference tree is absent (the GPU box)."""
 import os
 import re
+import shutil
+import subprocess
 
 import pytest
 
@@ -117,3 +121,12 @@ def test_recipe_names_the_reference_target_and_sources():
     for src in REPLACED:
         assert src in listed, f"{src} is not in the reference's strix_kernels sources"
         assert src in doc, f"the recipe does not name {src}"
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc absent")
+def test_shim_compiles_against_reference_headers(tmp_path):
+    (tmp_path / "format").write_text("")
+    cmd = ["hipcc", "-std=c++20", "-fsyntax-only", "--offload-arch=gfx950", f"-I{tmp_path}", f"-I{REF}",
+           f"-I{os.path.join(ROOT, 'include')}", SHIM]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-4000:]
