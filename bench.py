@@ -21,6 +21,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "µs/layer for q4 MoE verify at M=6 + achieved HBM GB/s; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 1_100_000_000  # weight replicas rotated by the dense GEMV lines: > 4x the 256 MB Infinity Cache
 TRAFFIC_JSON = os.path.join("profiles", "hbm_traffic_cfg3.json")
 COPY_PROBE_BYTES = 256 << 20  # FP32 elements read and written once by the calibration kernel
 
@@ -44,6 +45,8 @@ def parse():
                     help="only the dense prefill-width linears (for rocprofv3 runs): one JSON line with their timings")
     ap.add_argument("--tail-only", action="store_true",
                     help="only config 5's verify tail (for rocprofv3 runs): one JSON line with its timings")
+    ap.add_argument("--ceilings-only", action="store_true",
+                    help="only the streaming-read and MFMA probes (for rocprofv3 runs): one JSON line")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two --probe counter runs (FETCH_SIZE, WRITE_SIZE) into " + TRAFFIC_JSON)
     return ap.parse_args()
@@ -350,17 +353,20 @@ def extra_configs(out):
     from strixite_amd import synthetic as syn
 
     res = {}
-    # configs 1 and 2: dense q4 / q8 GEMV, 8 weight replicas rotated (> 256 MB Infinity Cache for config 2)
+    # configs 1 and 2: dense q4 / q8 GEMV over weight replicas rotated launch by launch, more than 1.1 GB of them
+    # (4x the 256 MB Infinity Cache), so every launch reads its weights from HBM
     for name, bits, N, K, G, M, act in (("cfg1_q4_4096x4096_M1_f32", 4, 4096, 4096, 128, 1, torch.float32),
                                         ("cfg2_q4_12288x4096_M6", 4, 12288, 4096, 128, 6, torch.bfloat16),
                                         ("cfg2_q8_12288x4096_M6", 8, 12288, 4096, 64, 6, torch.bfloat16)):
-        reps = [syn.qweight(bits, N, K, G, seed=30 + i) for i in range(8 if N > 4096 else 32)]
+        one = N * K * bits // 8 + 4 * N * (K // G)
+        reps = [syn.qweight(bits, N, K, G, seed=30 + i) for i in range(-(-ROTATE_BYTES // one))]
         x = syn.activations(M, K, seed=40, dtype=act)
         y = torch.empty((M, N), dtype=torch.float32, device="cuda")
         ms = time_window(lambda i: kx.linear(x, reps[i % len(reps)], out_act=0, y=y))
         nbytes = reps[0].nbytes() + x.numel() * x.element_size() + y.numel() * 4
         res[name] = {"us": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "rotated_MB": round(len(reps) * reps[0].nbytes() / 1e6)}
         del reps
     # config 4: the MoE layer at prefill width, M = 2048, Zipf-skewed routing; grouped MFMA experts
     res.update(dense_prefill())
@@ -368,6 +374,7 @@ def extra_configs(out):
     res["cfg5_verify_tail"] = verify_tail()
     res["mtp_draft_head"] = draft_head()
     out["configs"] = res
+    out["ceilings"] = ceilings()
 
 
 def dense_prefill():
@@ -387,6 +394,38 @@ def dense_prefill():
             "us": round(ms * 1e3, 1), "mfma_frac": round(2.0 * 2048 * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
         del w, x, y
     return res
+
+
+def ceilings():
+    """The part's own ceilings: a streaming read of 1 GiB (4x the Infinity Cache, so every byte comes from HBM) at a few
+    grid sizes, and a loop of independent BF16 MFMAs on every SIMD (sx_probe_stream_read, sx_probe_mfma)."""
+    import ctypes
+
+    import torch
+
+    import strixite_amd as sx
+    L = sx.lib()
+    nbytes = 1 << 30
+    buf = torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    read = {}
+    for blocks in (256, 1024, 4096):
+        ms = time_window(lambda i: sx.check(L.sx_probe_stream_read(buf.data_ptr(), nbytes, blocks, sink.data_ptr(), st)),
+                         min_launches=20, min_ms=20.0, warm_ms=10.0, windows=3)
+        read[f"blocks_{blocks}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    del buf
+    fl = ctypes.c_double()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    mfma = {}
+    for per_cu in (2, 4):
+        blocks = cus * per_cu
+        ms = time_window(lambda i: sx.check(L.sx_probe_mfma(blocks, 4096, sink.data_ptr(), ctypes.byref(fl), st)),
+                         min_launches=10, min_ms=20.0, warm_ms=10.0, windows=3)
+        mfma[f"waves_per_simd_{per_cu}"] = round(fl.value / (ms * 1e-3) / 1e12, 1)
+    return {"stream_read_GBps": read, "stream_read_bytes": nbytes, "stream_read_best_frac": round(
+                max(read.values()) / HBM_PEAK_GBS, 4),
+            "mfma_bf16_TFLOPs": mfma, "mfma_best_frac": round(max(mfma.values()) / 2500.0, 4)}
 
 
 def verify_tail():
@@ -542,6 +581,9 @@ def main():
         return
     if args.dense_only:
         print(json.dumps(dense_prefill()))
+        return
+    if args.ceilings_only:
+        print(json.dumps({"ceilings": ceilings()}))
         return
 
     out = {"metric": METRIC, "value": None, "unit": "us/layer", "n_gpus": 1, "steps": args.steps,

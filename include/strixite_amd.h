@@ -315,6 +315,15 @@ int sx_strixw_qview(const sx_strixw *f, const void *base, const char *name, int 
 int sx_strixw_data(const sx_strixw *f, const void *base, const char *name, int encoding, const int64_t *shape,
                    int ndim, const void **out);
 
+/* ---------------- measurement probes (no counterpart in the reference: the ceilings the roofline fractions are
+ * judged against, measured on the part) ---------------- */
+/* A streaming read of `bytes` (16-byte aligned) by `blocks` blocks of 512 threads, 16-byte loads, nothing stored
+ * (sink: 4 bytes, written only in a case the data practically never gives). */
+int sx_probe_stream_read(const void *buf, uint64_t bytes, int blocks, uint32_t *sink, sx_stream stream);
+/* `blocks` blocks of 4 waves, each wave `iters` x 4 independent v_mfma_f32_32x32x16_bf16; *flops (may be NULL) = the
+ * launch's dense BF16 flops. */
+int sx_probe_mfma(int blocks, int iters, float *sink, double *flops, sx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

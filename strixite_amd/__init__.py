@@ -114,6 +114,8 @@ SIGNATURES = {
     "sx_strixw_load": [_P, _P, _U64, _INT, ctypes.POINTER(_D), _P],
     "sx_strixw_qview": [_P, _P, _CP, _INT, _I64, _I64, _QV],
     "sx_strixw_data": [_P, _P, _CP, _INT, _PI64, _INT, ctypes.POINTER(_P)],
+    "sx_probe_stream_read": [_P, _U64, _INT, _P, _P],
+    "sx_probe_mfma": [_INT, _INT, _P, ctypes.POINTER(_D), _P],
 }
 _RESTYPES = {"sx_last_error": ctypes.c_char_p, "sx_version": ctypes.c_char_p, "sx_strix_hash64": _U64,
              "sx_strixw_close": None}

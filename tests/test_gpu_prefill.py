@@ -3,7 +3,8 @@ d = 4096, E = 512, top-10, I = 1024, q4 G = 128, routing skewed by a seeded Zipf
 prefill width (the route the reference's linear_q4_wmma / linear_q8_wmma callers take, kernels/linear_wmma.hpp:22-25).
 
 The oracle recomputes the router logits in full, the routing bit-exact on the GPU's logits, the grouping invariants
-on all 20,480 slots, and h and y for a seeded sample of tokens (every expert those tokens touch)."""
+on all 20,480 slots, h of every token on 128 seeded features and in full for 32 seeded tokens, and y for 256 seeded
+tokens (every expert those tokens touch)."""
 import numpy as np
 import pytest
 
@@ -107,9 +108,31 @@ def test_config4_prefill_layer_full_size():
     gh = util.host_bits(h)[toks]
     util.assert_close(gh, ref_h, roundings=4, what="config 4 h (sampled tokens)")
     del hgu
-    hdn = orc.QWeight(4, *cat(dn, d), U * d, I, 128)
-    ref_y, _ = orc.experts_combine(gh, hdn, U, rid, coef.cpu().numpy()[toks])
-    util.assert_close(util.host_bits(y)[toks], ref_y, what="config 4 y (sampled tokens)")
+    del gh
+
+    # h of every token and slot on 128 seeded features: the gate and up rows of those features of all 512 experts
+    J = np.sort(np.random.default_rng(67).choice(I, 128, replace=False))
+    rows = (np.arange(E)[:, None] * 2 * I + np.concatenate([J, I + J])[None, :]).ravel()
+    print(f"config 4: checking h of all {M} tokens on {len(J)} features", flush=True)
+    ridx = torch.from_numpy(rows).cuda()
+    qsub = gu.q.view(E * 2 * I, d // 2)[ridx].cpu().numpy().ravel()
+    ssub = gu.scale.view(E * 2 * I, d // 128)[ridx].cpu().numpy().view(np.uint16).ravel()
+    msub = gu.minv.view(E * 2 * I, d // 128)[ridx].cpu().numpy().view(np.uint16).ravel()
+    hsub = orc.QWeight(4, qsub, ssub, msub, len(rows), d, 128)
+    ref_hj, _ = orc.experts_gather(xh, hsub, E, g_ids, swiglu=True)
+    util.assert_close(util.host_bits(h)[:, :, J], ref_hj, roundings=4, what="config 4 h (all tokens, sampled features)")
+    del hsub, qsub, ssub, msub, ref_hj
+
+    # y of 256 seeded tokens from the GPU's h, against the oracle on the down rows of the experts they touch
+    ytoks = np.sort(np.random.default_rng(68).choice(M, 256, replace=False))
+    ysub = g_ids[ytoks]
+    ytouched = np.unique(ysub)
+    print(f"config 4: checking y of {len(ytoks)} tokens over {len(ytouched)} experts", flush=True)
+    yrid = np.searchsorted(ytouched, ysub).astype(np.int32)
+    hdn = orc.QWeight(4, *[np.concatenate(p) for p in zip(*[syn.host_rows(dn, e * d, (e + 1) * d) for e in ytouched])],
+                      len(ytouched) * d, I, 128)
+    ref_y, _ = orc.experts_combine(util.host_bits(h)[ytoks], hdn, len(ytouched), yrid, coef.cpu().numpy()[ytoks])
+    util.assert_close(util.host_bits(y)[ytoks], ref_y, what="config 4 y (sampled tokens)")
 
 
 @pytest.mark.parametrize("bits,G,act,out_act,M,K", [(4, 128, orc.BF16, orc.BF16, 2048, 4096),
@@ -154,3 +177,27 @@ def test_f32_x_prefill_keeps_full_precision():
     e_exact, e_round = util.max_abs_norm_err(got, exact), util.max_abs_norm_err(got, rounded)
     print(f"F32 x: error vs exact x {e_exact:.3g}, vs BF16-rounded x {e_round:.3g}", flush=True)
     assert e_exact < 1e-5 and e_round > 20 * e_exact
+
+
+@pytest.mark.parametrize("bits,G", [(4, 128), (8, 64)])
+def test_dense_prefill_bench_shape(bits, G):
+    """The dense prefill linears at the benchmarked shape (4096 x 4096, M = 2048, BF16 in and out) on the MFMA tiles:
+    every output feature of 256 seeded tokens, and every token on 128 seeded output features, against the oracle."""
+    import torch
+    from strixite_amd import synthetic as syn
+    N = K = 4096
+    M = 2048
+    w = syn.qweight(bits, N, K, G, seed=70 + bits)
+    x = syn.activations(M, K, seed=71 + bits)
+    print(f"dense prefill q{bits} at 4096 x 4096, M = 2048", flush=True)
+    y = kx().linear(x, w)
+    sync()
+    xh, yh = util.host_bits(x), util.host_bits(y)
+    toks = np.sort(np.random.default_rng(72).choice(M, 256, replace=False))
+    hw = orc.QWeight(bits, *syn.host_rows(w, 0, N), N, K, G)
+    util.assert_close(yh[toks], orc.linear_q(xh[toks], hw), what=f"dense q{bits} (256 tokens, all features)")
+    feats = np.sort(np.random.default_rng(73).choice(N, 128, replace=False))
+    per, groups = K * bits // 8, K // G
+    fw = orc.QWeight(bits, hw.q.reshape(N, per)[feats].ravel(), hw.scale.reshape(N, groups)[feats].ravel(),
+                     hw.minv.reshape(N, groups)[feats].ravel(), len(feats), K, G)
+    util.assert_close(yh[:, feats], orc.linear_q(xh, fw), what=f"dense q{bits} (all tokens, 128 features)")
