@@ -192,9 +192,15 @@ def moe_layer_bench(args, out):
     hh = [torch.randn((M, k, I), device="cuda").to(torch.bfloat16) for _ in range(R)]
     hs = [t.float().view(M * k, I // 16, 16).sum(-1) for t in hh]  # the 16-feature sums gate_up hands over
     yb = torch.empty((M, d), dtype=torch.bfloat16, device="cuda")
+    plans = []  # the routing plan gate_up hands over, one per batch
+    for r in range(R):
+        plans.append(kx.verify_plan())
+        kx.verify_gate_up(xs[r], routes[r][3], gu, E, k, ids=ids_b, coef=coef_b, h=h, router_err=rerr,
+                          expert_err=eerr, h_sums=h_sums, plan=plans[r])
 
     def down(i):
-        kx.verify_down(hh[i % R], dn, routes[i % R][0], routes[i % R][1], E, y=yb, expert_err=eerr, h_sums=hs[i % R])
+        kx.verify_down(hh[i % R], dn, routes[i % R][0], routes[i % R][1], E, y=yb, expert_err=eerr, h_sums=hs[i % R],
+                       plan=plans[i % R])
 
     ms_dn = time_window(down)
     dn_bytes = sum(down_bytes(Us[r], dn.nbytes() // E, M, d, k, I) for r in range(R)) / R

@@ -107,16 +107,20 @@ int sx_moe_verify_supported(int64_t M, int64_t A, int64_t E, int64_t k, int64_t 
  * sx_moe_verify_layer_sync_bytes bytes as sx_moe_verify_layer takes it (zeroed once, one per stream, may be the same
  * buffer): with K = 4096 each compute unit then streams a fixed run of about 4/5 of an equal share of the weight
  * tiles and takes the rest from a shared pool, so faster ones take more (without it each takes a fixed equal
- * share); the outputs are the same either way. */
+ * share); the outputs are the same either way. plan (nullable): a device buffer of SX_VERIFY_PLAN_BYTES bytes,
+ * 16-byte aligned, that receives the launch's routing in the form sx_moe_verify_down takes it. */
+#define SX_VERIFY_PLAN_BYTES 4096
 int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
                           const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *gate_up,
                           int64_t Ew, int32_t *ids, float *coef, void *h, float *h_sums, int act,
-                          uint32_t *router_err, uint32_t *expert_err, void *sync, sx_stream stream);
+                          uint32_t *router_err, uint32_t *expert_err, void *sync, void *plan, sx_stream stream);
 /* y [M, N] = sum_a coef[m, a] * (h[m, a] W_down[ids[m, a]]^T); NaN rows for tokens with an invalid slot. h_sums
- * (nullable): the h_sums sx_moe_verify_gate_up wrote with this h (saves the kernel summing h itself). */
+ * (nullable): the h_sums sx_moe_verify_gate_up wrote with this h (saves the kernel summing h itself). plan
+ * (nullable): the plan sx_moe_verify_gate_up wrote with these ids and coef; the launch then takes the routing from
+ * it (ids and coef are not read) instead of rebuilding the expert list, so its first weight loads go out sooner. */
 int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A, const int32_t *ids,
                        const float *coef, const sx_qview *down, int64_t Ew, void *y, int act, uint32_t *expert_err,
-                       sx_stream stream);
+                       const void *plan, sx_stream stream);
 /* ---- the whole verify-width MoE sublayer in one launch ----
  * runtime/qwen4exp.cpp:1132-1163 below kGroupedMinTokens - the router projection (linear_bf16w, kernels/linear.hpp:19-24,
  * or an FP32 weight), moe_router (moe_router.hpp:38-40), linear_q4_experts_gather_swiglu (linear_q4.hpp:55-56) and

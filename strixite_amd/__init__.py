@@ -85,8 +85,8 @@ SIGNATURES = {
     "sx_moe_router_group": [_P, _I64, _I64, _I64, _I64, _INT, _P, _P, _P, _P, ctypes.c_size_t, _P, _P],
     "sx_moe_verify_supported": [_I64, _I64, _I64, _I64, _I64, _QV, _QV, _INT],
     "sx_moe_verify_gate_up": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _INT, _QV, _I64, _P, _P, _P, _P, _INT, _P, _P,
-                              _P, _P],
-    "sx_moe_verify_down": [_P, _P, _I64, _I64, _P, _P, _QV, _I64, _P, _INT, _P, _P],
+                              _P, _P, _P],
+    "sx_moe_verify_down": [_P, _P, _I64, _I64, _P, _P, _QV, _I64, _P, _INT, _P, _P, _P],
     "sx_moe_verify_layer_sync_bytes": [_SZP],
     "sx_moe_verify_layer_trace": [_P],
     "sx_moe_verify_layer": [_P, _I64, _P, _INT, _I64, _I64, _I64, _INT, ctypes.c_int32, _QV, _QV, _I64, _P, _P, _P, _P,

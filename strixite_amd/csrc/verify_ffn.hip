@@ -46,28 +46,32 @@ constexpr int kZeroBytes = qmm::detail::kZeroBytes;
 struct Routes {                // one block's copy of the routing (LDS)
     int32_t ids[kMaxSlots];    // slot s = m * A + a
     float coef[kMaxSlots];
-    int32_t u_exp[kMaxSlots + 1];  // distinct valid experts, ascending (entry kMaxSlots: a write sink)
-    uint32_t u_mask[kMaxSlots + 1];  // their tokens (bit m)
+    int32_t u_exp[kMaxSlots];  // distinct valid experts, ascending
+    uint32_t u_mask[kMaxSlots];  // their tokens (bit m)
     int U;
     uint64_t bad_slots;        // invalid slots: id outside [0, Ew) or repeated within its token
     int8_t slot_tab[kMaxSlots][kMaxTokens];  // [unit][token]: the token's slot of the unit's expert, or -1
 };
+// A block's routing as gate_up hands it to down: the Routes bytes, copied 16 bytes a thread.
+static_assert(sizeof(Routes) % 16 == 0 && sizeof(Routes) <= SX_VERIFY_PLAN_BYTES, "the plan holds a Routes");
+constexpr int kPlanQuads = (int)(sizeof(Routes) / 16);
+static_assert(kPlanQuads <= kThreads, "one 16-byte copy a thread");
 
 // The distinct experts of the slots in id order with their token masks. bad_slots marks ids outside [0, Ew) and
 // repeats of an id within a token (the routers never produce one; such a slot is treated as invalid: the later
 // slot of the two). Wave 0 alone does it, from `id` = its lane's slot id (lane < S): the LDS operations of one wave
-// take effect in program order, so no barrier is needed until the closing one. Lane t owns experts kPer t ..
-// kPer t + kPer - 1: their token masks in four 16-byte reads, a wave prefix sum of the counts placing its units.
+// take effect in program order, so no barrier is needed until the closing one. Every LDS access is conflict-free:
+// the token-mask table is cleared and read a 64-expert row at a time (lane l: expert 64 q + l), each row's present
+// experts form a ballot, and a unit's index is the count of present experts before it (the earlier rows' counts, a
+// scalar running sum, plus the lane's rank in its row's ballot); only present experts write their unit.
 // emask: LDS [kMaxExperts], 16-byte aligned. Ends with an LDS-only block barrier.
 __device__ void build_units(Routes &R, uint32_t *emask, int32_t id, int S, int A, int Ew) {
-    constexpr int kPer = kMaxExperts / 64, kQuads = kPer / 4;
-    static_assert(kPer % 4 == 0, "experts a lane: whole 16-byte words");
+    constexpr int kRows = kMaxExperts / 64;
     static_assert(kMaxSlots * kMaxTokens == 64 * 16, "slot_tab: one 16-byte row a lane");
     const int t = threadIdx.x;
     if (t < 64) {
-        uint4 *mine = reinterpret_cast<uint4 *>(emask) + t * kQuads;
 #pragma unroll
-        for (int q = 0; q < kQuads; ++q) mine[q] = uint4{0u, 0u, 0u, 0u};
+        for (int q = 0; q < kRows / 4; ++q) reinterpret_cast<uint4 *>(emask)[q * 64 + t] = uint4{0u, 0u, 0u, 0u};
         reinterpret_cast<int4 *>(&R.slot_tab[0][0])[t] = make_int4(-1, -1, -1, -1);
         const bool in = t < S;
         bool bad = in && !(id >= 0 && id < Ew);
@@ -81,26 +85,21 @@ __device__ void build_units(Routes &R, uint32_t *emask, int32_t id, int S, int A
             }
         }
         const uint64_t bad_mask = __ballot(bad);
-        uint32_t mk[kPer];
+        uint32_t mk[kRows];
 #pragma unroll
-        for (int q = 0; q < kQuads; ++q) {
-            const uint4 w = mine[q];
-            mk[4 * q] = w.x, mk[4 * q + 1] = w.y, mk[4 * q + 2] = w.z, mk[4 * q + 3] = w.w;
+        for (int q = 0; q < kRows; ++q) mk[q] = emask[q * 64 + t];
+        int base = 0;  // wave-uniform: units before row q
+#pragma unroll
+        for (int q = 0; q < kRows; ++q) {
+            const uint64_t present = __ballot(mk[q] != 0u);
+            if (mk[q] != 0u) {
+                const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(present >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)present, 0u));
+                R.u_exp[pos] = q * 64 + t, R.u_mask[pos] = mk[q], emask[q * 64 + t] = (uint32_t)pos;
+            }
+            base += __popcll(present);
         }
-        uint32_t c = 0u;
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) c += mk[j] != 0u;
-        const uint32_t incl = routing::wave_incl_scan_u32(c);
-        int pos = (int)(incl - c);
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) {  // branch-free: an expert with no token writes to the sink entry
-            const bool on = mk[j] != 0u;
-            const int at = on ? pos : kMaxSlots;
-            R.u_exp[at] = kPer * t + j, R.u_mask[at] = mk[j], emask[kPer * t + j] = (uint32_t)pos;
-            pos += on ? 1 : 0;
-        }
-        if (t == 63) R.U = (int)incl;
-        if (t == 0) R.bad_slots = bad_mask;
+        if (t == 0) R.U = base, R.bad_slots = bad_mask;
         if (in && !bad) R.slot_tab[emask[id]][t / A] = (int8_t)t;
     }
     lds_barrier();  // the loads in flight (activations, weights) keep going
@@ -310,6 +309,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     const int U = __builtin_amdgcn_readfirstlane(R.U);
     const int64_t Nrows = p.N / 2, rowbytes = K / 2, ngroups = K / kSpan;
     if (lead) {
+        if (p.plan && tid < kPlanQuads) reinterpret_cast<uint4 *>(p.plan)[tid] = reinterpret_cast<const uint4 *>(&R)[tid];
         if (tid < S) p.ids[tid] = R.ids[tid], p.coef[tid] = R.coef[tid];
         uint64_t bad = R.bad_slots;  // invalid slots: error words (first slot wins) and NaN rows
         if (bad && tid == 0) {
@@ -617,6 +617,15 @@ __device__ __forceinline__ void down_body(const DownParams &p, DnLds &L, Routes 
         }
     };
     if constexpr (!FUSED) {
+        if (p.plan) {  // gate_up's routing as it stored it: one 16-byte load a thread, no rebuilding
+            const uint4 r = reinterpret_cast<const uint4 *>(p.plan)[min(tid, kPlanQuads - 1)];
+            load_h();
+            if (tid < kPlanQuads) reinterpret_cast<uint4 *>(&R)[tid] = r;
+            for (int i = tid; i < kZeroBytes / 4; i += kThreads) reinterpret_cast<uint32_t *>(L.zero_block)[i] = 0u;
+            lds_barrier();
+        }
+    }
+    if constexpr (!FUSED) if (!p.plan) {
         // the routing first, then the rows of h: the grouping waits for the ids only
         const int32_t my_id = p.ids[min(lane, S - 1)];  // every wave: no branch around loads
         const float my_coef = p.coef[min(lane, S - 1)];
@@ -1096,7 +1105,7 @@ int sx_moe_verify_supported(int64_t M, int64_t A, int64_t E, int64_t k, int64_t 
 int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t ld, int64_t E, int64_t k,
                           const float *shared_logit, int64_t shared_ld, int32_t shared_id, const sx_qview *w, int64_t Ew,
                           int32_t *ids, float *coef, void *h, float *h_sums, int act, uint32_t *router_err,
-                          uint32_t *expert_err, void *sync, sx_stream stream) {
+                          uint32_t *expert_err, void *sync, void *plan, sx_stream stream) {
     const char *fn = "sx_moe_verify_gate_up";
     const int64_t A = k + (shared_logit ? 1 : 0);
     SX_CHECK(x != nullptr && logits != nullptr && ids != nullptr && coef != nullptr && h != nullptr &&
@@ -1116,6 +1125,8 @@ int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t
     p.logits = logits, p.ld = ld, p.shared_logit = shared_logit, p.shared_ld = shared_ld, p.shared_id = shared_id;
     p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = w->N / Ew, p.K = w->K;
     p.ids = ids, p.coef = coef, p.h = static_cast<uint16_t *>(h), p.h_sums = h_sums, p.router_err = router_err, p.expert_err = expert_err;
+    SX_CHECK(plan == nullptr || aligned(plan, 16), fn, " plan must be 16-byte aligned");
+    p.plan = plan;
     // The pool schedule exists for K = 4096 (eight K slices a block); other shapes split the items statically and
     // leave the buffer untouched.
     if (sync != nullptr && w->K == 4096) {
@@ -1129,7 +1140,8 @@ int sx_moe_verify_gate_up(const void *x, int64_t M, const float *logits, int64_t
 }
 
 int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A, const int32_t *ids, const float *coef,
-                       const sx_qview *w, int64_t Ew, void *y, int act, uint32_t *expert_err, sx_stream stream) {
+                       const sx_qview *w, int64_t Ew, void *y, int act, uint32_t *expert_err, const void *plan,
+                       sx_stream stream) {
     const char *fn = "sx_moe_verify_down";
     SX_CHECK(h != nullptr && ids != nullptr && coef != nullptr && y != nullptr && expert_err != nullptr, fn,
              " null pointer");
@@ -1141,6 +1153,8 @@ int sx_moe_verify_down(const void *h, const float *h_sums, int64_t M, int64_t A,
     p.h = static_cast<const uint16_t *>(h), p.h_sums = h_sums, p.M = (int)M, p.A = (int)A, p.Ew = (int)Ew, p.ids = ids, p.coef = coef;
     p.q = w->q, p.scale = w->scale, p.minv = w->minv, p.N = N, p.K = w->K, p.y = y, p.act = act;
     p.expert_err = expert_err;
+    SX_CHECK(plan == nullptr || aligned(plan, 16), fn, " plan must be 16-byte aligned");
+    p.plan = plan;
     SX_HIP(vf::launch_down(p, stream_of(stream)), fn);
     return SX_OK;
 }

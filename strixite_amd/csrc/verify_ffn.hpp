@@ -31,6 +31,7 @@ struct GateUpParams {
     uint32_t *router_err, *expert_err;
     LayerSync *sync;    // nullable: after a fixed run a block, items from the pool counter of its set epoch & 1
     uint32_t epoch;
+    void *plan;         // nullable: block 0 stores its routing (ids, coef, the expert list, slot table) here for down
 };
 
 struct DownParams {
@@ -45,6 +46,7 @@ struct DownParams {
     void *y;            // [M, N] in act
     int act;
     uint32_t *expert_err;
+    const void *plan;   // nullable: gate_up's stored routing, taken as is instead of rebuilding it from ids / coef
 };
 
 // The one-launch layer's shared state: block b stores the launch's epoch (numbered by the host, never 0) into its

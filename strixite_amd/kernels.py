@@ -132,11 +132,12 @@ def verify_supported(M, A, E, k, Ew, gate_up, down, act=ACT_BF16):
 
 
 def verify_gate_up(x, logits, w, E, k, Ew=None, shared_logit=None, shared_id=0, ids=None, coef=None, h=None,
-                   router_err=None, expert_err=None, h_sums=None, sync=None, stream=None):
+                   router_err=None, expert_err=None, h_sums=None, sync=None, plan=None, stream=None):
     """moe_router + gather_swiglu in one launch at verify width: ids, coef [M, A], h [M, A, I]. h_sums (optional,
     FP32 [M * A, ceil(I / 16)]) receives the 16-feature sums of h that verify_down can take. sync (optional,
     verify_layer_sync(), one per stream): after a fixed run each compute unit takes weight tiles from a shared pool
-    (K = 4096), so the faster ones take more; same outputs."""
+    (K = 4096), so the faster ones take more; same outputs. plan (optional, verify_plan()) receives the routing in
+    the form verify_down takes it."""
     M, ld = x.shape[0], logits.stride(0)
     Ew = E if Ew is None else Ew
     A = k + (shared_logit is not None)
@@ -150,20 +151,28 @@ def verify_gate_up(x, logits, w, E, k, Ew=None, shared_logit=None, shared_id=0, 
     sld = 0 if shared_logit is None else shared_logit.stride(0)
     check(lib().sx_moe_verify_gate_up(_p(x), M, _p(logits), ld, E, k, _p(shared_logit), sld, shared_id, w.view(), Ew,
                                       _p(ids), _p(coef), _p(h), _p(h_sums), act_of(x), _p(router_err),
-                                      _p(expert_err), _p(sync), _s(stream)))
+                                      _p(expert_err), _p(sync), _p(plan), _s(stream)))
     return ids, coef, h, router_err, expert_err
 
 
-def verify_down(h, w, ids, coef, Ew, y=None, expert_err=None, h_sums=None, stream=None):
+def verify_down(h, w, ids, coef, Ew, y=None, expert_err=None, h_sums=None, plan=None, stream=None):
     """y[M, N] = sum_a coef[m, a] * (h[m, a] . W[ids[m, a]]) in one launch at verify width (h_sums: verify_gate_up's
-    sums of this h, optional)."""
+    sums of this h, optional; plan: the routing plan verify_gate_up stored with these ids, optional)."""
     M, A = ids.shape
     N = w.N // Ew
     y = torch.empty((M, N), dtype=h.dtype, device=h.device) if y is None else y
     expert_err = _err(h.device) if expert_err is None else expert_err
     check(lib().sx_moe_verify_down(_p(h), _p(h_sums), M, A, _p(ids), _p(coef), w.view(), Ew, _p(y), act_of(h),
-                                   _p(expert_err), _s(stream)))
+                                   _p(expert_err), _p(plan), _s(stream)))
     return y, expert_err
+
+
+VERIFY_PLAN_BYTES = 4096  # SX_VERIFY_PLAN_BYTES
+
+
+def verify_plan(device="cuda"):
+    """A buffer for the routing plan verify_gate_up stores and verify_down takes."""
+    return torch.empty(VERIFY_PLAN_BYTES // 4, dtype=torch.int32, device=device)
 
 
 def verify_layer_sync(device="cuda"):

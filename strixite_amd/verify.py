@@ -37,6 +37,7 @@ class MoeVerifyLayer:
         # the gate_up pool's sync buffers, one per stream: launches on one buffer must run in order, which only one
         # stream guarantees
         self._syncs = {}
+        self.plan = kx.verify_plan(dev)  # the routing gate_up hands to down (written and read in stream order)
         self._dev = dev
 
     def _sync_for(self, stream):
@@ -56,9 +57,9 @@ class MoeVerifyLayer:
         if self._fused(M):
             kx.verify_gate_up(x, self.logits[:M], self.gate_up, self.E, self.k, ids=self.ids[:M], coef=self.coef[:M],
                               h=self.h[:M], router_err=self.router_err, expert_err=self.expert_err,
-                              h_sums=self.h_sums, sync=self._sync_for(stream), stream=stream)
+                              h_sums=self.h_sums, sync=self._sync_for(stream), plan=self.plan, stream=stream)
             kx.verify_down(self.h[:M], self.down, self.ids[:M], self.coef[:M], self.E, y=self.y[:M],
-                           expert_err=self.expert_err, h_sums=self.h_sums, stream=stream)
+                           expert_err=self.expert_err, h_sums=self.h_sums, plan=self.plan, stream=stream)
             return self.y[:M]
         if M * self.k <= 2048:  # top-k + grouping in one launch
             kx.router_group(self.logits[:M], self.E, self.k, ws=ws, ids=self.ids[:M], coef=self.coef[:M],

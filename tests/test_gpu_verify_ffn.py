@@ -38,10 +38,16 @@ def run_fused(x, L, wgu, wdn, E, k, shared, sums=True):
     M, I = x.shape[0], wdn.K
     A = k + (1 if shared else 0)
     hs = torch.full((M * A, I // 16), float("nan"), dtype=torch.float32, device="cuda") if sums else None
+    plan = kx().verify_plan()
     ids, coef, h, rerr, eerr = kx().verify_gate_up(util.bf16_dev(x), Ld, Wgu, E, k, Ew=Ew, shared_logit=sl,
-                                                   shared_id=E, h_sums=hs)
+                                                   shared_id=E, h_sums=hs, plan=plan)
     y, _ = kx().verify_down(h, Wdn, ids, coef, Ew, expert_err=eerr, h_sums=hs)
+    # the same down taking gate_up's plan instead of rebuilding the routing from ids / coef: the same bits
+    eerr_p = torch.zeros(4, dtype=torch.int32, device="cuda")
+    y_p, _ = kx().verify_down(h, Wdn, ids, coef, Ew, expert_err=eerr_p, h_sums=hs, plan=plan)
     sync()
+    assert torch.equal(y.view(torch.int16), y_p.view(torch.int16)), "down with the plan differs"
+    assert torch.equal(eerr[:3], eerr_p[:3]), "down with the plan reports other errors"
     hb = util.host_bits(h)
     if sums:
         hf = util.as_f32(hb).reshape(M * A, I // 16, 16).astype(np.float64)
