@@ -236,6 +236,18 @@ int sx_mtp_pick_ws(const float *logits, int64_t n, const uint32_t *router_err, c
                    const uint32_t *attn_err, const unsigned long long *emb_err, sx_mtp_pick_t *out, void *workspace,
                    size_t workspace_bytes, sx_stream stream);
 
+/* ---- logits top-k and acceptance in one launch (the verify tail after the LM head) ----
+ * sx_logits_topk (kernels/logits_topk.hpp:35-46) followed by sx_mtp_accept (serve/engine.cpp:592-653 with
+ * serve/sampler.cpp:183-248), as one kernel whose blocks hand over through counters in `workspace`; no reference
+ * counterpart as one call. cands / nan: as sx_logits_topk's out / nan (k = kc), for every row. out (nullable: top-k
+ * only): as sx_mtp_accept's, for drafts [k] (rows >= k + 1). workspace: sx_verify_tail_workspace_bytes bytes, 8-byte
+ * aligned, ZEROED before its first use (it holds counters each launch leaves at zero); one per stream. Shapes whose
+ * first level leaves more than 4096 candidates a row are refused (sx_logits_topk takes them). */
+int sx_verify_tail_workspace_bytes(int64_t rows, int64_t n_valid, int64_t kc, size_t *bytes);
+int sx_verify_tail(const float *logits, int64_t rows, int64_t ld, int64_t n_valid, int64_t kc, sx_logit_cand *cands,
+                   uint32_t *nan, const uint32_t *mask, int64_t mask_words, const int32_t *drafts, int64_t k,
+                   const double *u, double temperature, int64_t top_k, double top_p, int32_t *out, void *workspace,
+                   size_t workspace_bytes, sx_stream stream);
 /* ---- draft acceptance on the device: serve/engine.cpp:592-610 with Sampler semantics (serve/sampler.cpp:183-248) ----
  * cands [k+1, kc] (from sx_logits_topk, value desc), nan [k+1], drafts [k] (device). Row j is sampled (greedy:
  * candidate 0; else temperature -> top_k (<= kc) -> top_p -> draw r = u[j] * kept, u[j] a host draw of

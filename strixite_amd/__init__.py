@@ -114,6 +114,9 @@ SIGNATURES = {
     "sx_strixw_load": [_P, _P, _U64, _INT, ctypes.POINTER(_D), _P],
     "sx_strixw_qview": [_P, _P, _CP, _INT, _I64, _I64, _QV],
     "sx_strixw_data": [_P, _P, _CP, _INT, _PI64, _INT, ctypes.POINTER(_P)],
+    "sx_verify_tail_workspace_bytes": [_I64, _I64, _I64, _SZP],
+    "sx_verify_tail": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _P, _D, _I64, _D, _P, _P,
+                       ctypes.c_size_t, _P],
     "sx_probe_stream_read": [_P, _U64, _INT, _P, _P],
     "sx_probe_mfma": [_INT, _INT, _P, ctypes.POINTER(_D), _P],
 }

@@ -103,6 +103,19 @@ __device__ __forceinline__ uint64_t wave_topk_sorted(const uint64_t (&key)[P], i
     return lane < k ? list : 0;
 }
 
+constexpr int kTopkThreadsB = 256;  // threads of a top-k block
+
+__device__ __forceinline__ uint32_t routing_wave_incl_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(v, off);
+        if (lane >= off) v += o;
+    }
+    return (uint32_t)v;
+}
+constexpr int kScratchB = 256;      // candidates a wave's region holds (keys)
+
 // wave_topk_sorted's result by ranks instead of sorts: the threshold T is the value word of the k-th best lane
 // maximum (a search two bits a step with ballots, over its top 16 bits: a T with its low bits cleared is still at
 // most that maximum, and admits only keys within 2^-7 of it besides), so every top-k key has a value word >= T; the keys that reach it
@@ -153,14 +166,111 @@ __device__ __forceinline__ uint64_t wave_topk(const uint64_t (&key)[P], int k, u
     return list;
 }
 
+// LDS of block_topk.
+struct BlockTopkLds {
+    uint64_t cand[kTopkThreadsB * 2];  // candidates (keys that reach the threshold), any order
+    uint32_t head[kTopkThreadsB];      // each thread's best value word
+    uint64_t best[64];
+    uint32_t T;
+    int n;
+};
+
+// The block's best k (k <= 64) of the keys its threads hold (P a thread, kTopkThreadsB threads), sorted descending:
+// lane l of every thread's wave returns key l of the list (0 past k or past the keys there are). The threshold T is
+// the value word of the k-th best of the threads' own best keys, found by wave 0 two bits a step with ballots over
+// its top 16 bits (a T with its low bits cleared is still at most that key, and admits only keys within 2^-7 of it
+// besides): at least k keys reach it, so every key of the top k does. The keys that reach it (about k for continuous
+// values) are compacted into LDS, and each is ranked against all of them by one thread with broadcast reads, eight
+// keys in flight (keys are unique: ids differ); the one of rank r < k is the block's r-th best. No sort and no merge.
+// More candidates than LDS holds (heavy ties at T) take the waves' own top-k lists, merged.
+template <int P>
+__device__ uint64_t block_topk(const uint64_t (&key)[P], int k, BlockTopkLds &L, uint64_t (*region)[kScratchB]) {
+    constexpr int kCap = kTopkThreadsB * 2;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    uint64_t head = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) head = umax(head, key[p]);
+    L.head[t] = (uint32_t)(head >> 32);
+    if (t == 0) L.n = 0;
+    if (t < 64) L.best[t] = 0;
+    __syncthreads();
+    if (wave == 0) {
+        constexpr int kH = kTopkThreadsB / 64;
+        uint32_t h[kH];
+#pragma unroll
+        for (int j = 0; j < kH; ++j) h[j] = L.head[lane + 64 * j];
+        uint32_t T = 0u;
+        for (int b = 30; b >= 16; b -= 2) {  // uniform
+            const uint32_t t1 = T | (1u << b), t2 = T | (2u << b), t3 = T | (3u << b);
+            int c1 = 0, c2 = 0, c3 = 0;
+#pragma unroll
+            for (int j = 0; j < kH; ++j)
+                c1 += __popcll(__ballot(h[j] >= t1)), c2 += __popcll(__ballot(h[j] >= t2)), c3 += __popcll(__ballot(h[j] >= t3));
+            T = c3 >= k ? t3 : c2 >= k ? t2 : c1 >= k ? t1 : T;
+        }
+        if (lane == 0) L.T = T;
+    }
+    __syncthreads();
+    const uint32_t T = L.T;
+    int mine = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) mine += (key[p] != 0 && (uint32_t)(key[p] >> 32) >= T) ? 1 : 0;
+    const uint32_t incl = routing_wave_incl_scan(mine);
+    int base = 0;
+    if (lane == 63) base = atomicAdd(&L.n, (int)incl);
+    base = __shfl(base, 63);
+    int at = base + (int)incl - mine;
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+        if (key[p] != 0 && (uint32_t)(key[p] >> 32) >= T) {
+            if (at < kCap) L.cand[at] = key[p];
+            ++at;
+        }
+    __syncthreads();
+    const int C = L.n;
+    if (C > kCap) {  // uniform over the block: heavy ties at T
+        const uint64_t w = wave_topk<P>(key, k, region[wave], kScratchB);
+        __syncthreads();
+        region[wave][lane] = w;
+        __syncthreads();
+        uint64_t list = region[0][lane];
+#pragma unroll
+        for (int v = 1; v < kTopkThreadsB / 64; ++v) {
+            list = wave_merge_desc(list, region[v][lane]);
+            list = lane < k ? list : 0;
+        }
+        __syncthreads();
+        return list;
+    }
+    for (int i = t; i < C; i += kTopkThreadsB) {
+        const uint64_t x = L.cand[i];
+        int rank = 0;
+        for (int c = 0; c < C; c += 8) {  // uniform; past C: ignored (reads stay inside cand)
+            ulonglong2 o[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) o[u] = *reinterpret_cast<const ulonglong2 *>(L.cand + min(c + 2 * u, kCap - 2));
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                rank += (c + 2 * u < C && o[u].x > x) ? 1 : 0;
+                rank += (c + 2 * u + 1 < C && o[u].y > x) ? 1 : 0;
+            }
+        }
+        if (rank < k) L.best[rank] = x;
+    }
+    __syncthreads();
+    const uint64_t r = lane < k ? L.best[lane] : 0;
+    __syncthreads();  // L and the regions are free for the caller's next use
+    return r;
+}
+
 // ---------------- logits top-k ----------------
 // One level: workgroup g of row r reduces up to kGroup inputs - logits (level 1: ids = positions < n_valid, NaN
 // flagged and left out, masked ids left out) or an earlier level's key lists - to its best k keys. Each wave takes a
 // strided quarter (coalesced loads), finds its best k (wave_topk), and wave 0 merges the four lists.
-constexpr int kTopkThreads = 256;
+constexpr int kTopkThreads = kTopkThreadsB;
 constexpr int kPer = 16;                      // inputs a thread holds
 constexpr int kGroup = kTopkThreads * kPer;   // inputs a workgroup reduces
-constexpr int kScratch = 256;                 // compaction room a wave (keys)
+constexpr int kScratch = kScratchB;           // compaction room a wave (keys)
 
 template <bool kLogits, bool kMasked>
 __global__ void __launch_bounds__(kTopkThreads)
@@ -170,6 +280,7 @@ __global__ void __launch_bounds__(kTopkThreads)
     __shared__ uint64_t scratch[kTopkThreads / 64][kScratch];
     __shared__ uint64_t lists[kTopkThreads / 64][64];
     __shared__ uint32_t s_nan;
+    __shared__ BlockTopkLds s_btk;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = blockIdx.x;
     const int64_t r = blockIdx.y;
     if (t == 0) s_nan = 0;
@@ -211,16 +322,8 @@ __global__ void __launch_bounds__(kTopkThreads)
         for (int c = lane; c < groups1; c += 64) f1 |= nan_level1[r * groups1 + c] != 0u;
     __syncthreads();
     if (my_nan) atomicOr(&s_nan, 1u);
-    const uint64_t mine = wave_topk<kPer>(key, k, scratch[wave], kScratch);
-    lists[wave][lane] = mine;
-    __syncthreads();
+    const uint64_t best = block_topk<kPer>(key, k, s_btk, scratch);
     if (wave != 0) return;
-    uint64_t best = lists[0][lane];
-#pragma unroll
-    for (int w = 1; w < kTopkThreads / 64; ++w) {
-        best = wave_merge_desc(best, lists[w][lane]);
-        best = lane < k ? best : 0;
-    }
     if (groups > 1) {
         if (lane < k) out_keys[(r * groups + g) * k + lane] = best;
     } else if (lane < k) {  // the last level: candidates with their values from the keys (a zero read back from the
@@ -375,35 +478,50 @@ __global__ void __launch_bounds__(kPickWsThreads) mtp_pick_ws_kernel(const float
 // same double arithmetic, once each) before lane 0's sequential walk reads them; once lane 0 has their sum, the
 // quotients p_i / sum the top-p walk adds are taken a lane each too (each quotient is the same division whoever
 // makes it, so the walk's sums are unchanged).
-__global__ void __launch_bounds__(64)
-    mtp_accept_kernel(const sx_logit_cand *cands, const uint32_t *nan, int kc, const int32_t *drafts, int k,
-                      const double *u, double temperature, int top_k, double top_p, int64_t n_valid, int32_t *out) {
-    __shared__ sx_logit_cand cs[64];
-    __shared__ double probs[64], quot[64], s_sum;
-    __shared__ int s_go;
-    const int lane = threadIdx.x;
+// LDS of one acceptance walk.
+struct AcceptLds {
+    sx_logit_cand cs[64];
+    double probs[64], quot[64], sum;
+    int go;
+};
+
+// Ordering among the lanes of one wave through LDS (the walk runs on one wave).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// The walk by one wave; cand(j, i) and nan_of(j) read row j's candidate i and NaN flag.
+template <typename CandAt, typename NanAt>
+__device__ void accept_walk(CandAt cand, NanAt nan_of, int kc, const int32_t *drafts, int k, const double *u,
+                            double temperature, int top_k, double top_p, int64_t n_valid, int32_t *out, AcceptLds &L) {
+    sx_logit_cand *cs = L.cs;
+    double *probs = L.probs, *quot = L.quot;
+    const int lane = threadIdx.x & 63;
     const int kk = (int)(top_k < n_valid ? top_k : n_valid);
     int status = 0, j = 0;
     for (;; ++j) {
-        if (lane < kc) cs[lane] = cands[(int64_t)j * kc + lane];
-        __syncthreads();
+        if (lane < kc) cs[lane] = cand(j, lane);
+        const bool row_nan = nan_of(j) != 0u;
+        wave_sync();
         const bool sampled = temperature != 0 && isfinite(cs[0].v);  // uniform
         if (sampled && lane < kk) probs[lane] = exp((double)cs[lane].v / temperature - (double)cs[0].v / temperature);
-        __syncthreads();
+        wave_sync();
         if (sampled && top_p < 1) {
             if (lane == 0) {
                 double sum = 0;
                 for (int i = 0; i < kk; ++i) sum += probs[i];
-                s_sum = sum;
+                L.sum = sum;
             }
-            __syncthreads();
-            if (lane < kk) quot[lane] = probs[lane] / s_sum;
-            __syncthreads();
+            wave_sync();
+            if (lane < kk) quot[lane] = probs[lane] / L.sum;
+            wave_sync();
         }
         if (lane == 0) {
             const sx_logit_cand *c = cs;
             int32_t v = -1;
-            bool ok = nan[j] == 0;
+            bool ok = !row_nan;
             // serve/sampler.cpp:192-201: real candidates (ids in range) first, then only padding; at least one real.
             bool padding = false;
             const int m = kc < 20 ? kc : 20;
@@ -452,12 +570,170 @@ __global__ void __launch_bounds__(64)
                 out[2 + j] = v;
                 go = !(j == k || v != drafts[j]);
             }
-            s_go = go ? 1 : 0;
+            L.go = go ? 1 : 0;
         }
-        __syncthreads();
-        if (!s_go) break;
+        wave_sync();
+        if (!L.go) break;
     }
     if (lane == 0) out[0] = j, out[1] = status;
+}
+
+__global__ void __launch_bounds__(64)
+    mtp_accept_kernel(const sx_logit_cand *cands, const uint32_t *nan, int kc, const int32_t *drafts, int k,
+                      const double *u, double temperature, int top_k, double top_p, int64_t n_valid, int32_t *out) {
+    __shared__ AcceptLds L;
+    accept_walk([&](int j, int i) { return cands[(int64_t)j * kc + i]; }, [&](int j) { return nan[j]; }, kc, drafts,
+                k, u, temperature, top_k, top_p, n_valid, out, L);
+}
+
+// ---------------- logits top-k and acceptance in one launch ----------------
+// The verify tail after the LM head. Block (g, r) takes the first level's group g of row r exactly as
+// topk_level_kernel does and publishes its best k keys and its NaN flag at agent scope (the blocks run on different
+// XCDs, whose L2 caches are not coherent with each other), then counts itself in the row's counter once those stores
+// have completed. The row's last block reads the row's g1 k keys back (agent scope), reduces them to the final k the
+// same way (a wave's best k of its strided share, four lists merged), writes the candidates and the row's NaN flag,
+// and counts the row done; the last row's block walks the acceptance on one wave, from the candidates as the other
+// blocks stored them. Counters: zero before the first launch, each set back to zero by the block that read it last.
+struct TailArgs {
+    const float *logits;
+    int64_t ld;
+    int n_valid, g1, k, rows;
+    const uint32_t *mask;
+    int64_t mask_words;
+    uint64_t *keys;    // [rows][g1][k]
+    uint32_t *nan1;    // [rows][g1]
+    uint32_t *count;   // [rows + 1]
+    sx_logit_cand *cands;
+    uint32_t *nan;
+    const int32_t *drafts;
+    int nd;
+    const double *u;
+    double temperature;
+    int top_k;
+    double top_p;
+    int32_t *out;
+};
+
+__device__ __forceinline__ void store_agent64(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_agent64(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_agent32(const uint32_t *p) {
+    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The candidate a final key stands for: padding (-inf, INT32_MAX) for 0, else the key's value and id (a zero is read
+// back from the row: the key folds -0 onto +0).
+__device__ __forceinline__ sx_logit_cand cand_of(uint64_t best, const float *row) {
+    sx_logit_cand c;
+    if (best == 0) {
+        c.v = -INFINITY, c.id = INT32_MAX;
+    } else {
+        const uint32_t hi = (uint32_t)(best >> 32);
+        c.id = key_id(best);
+        c.v = __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
+        if (c.v == 0.f) c.v = row[c.id];
+    }
+    return c;
+}
+
+template <bool kMasked>
+__global__ void __launch_bounds__(kTopkThreads) topk_accept_kernel(TailArgs a) {
+    __shared__ uint64_t scratch[kTopkThreads / 64][kScratch];
+    __shared__ uint64_t lists[kTopkThreads / 64][64];
+    __shared__ uint32_t s_nan;
+    __shared__ int s_last;
+    __shared__ BlockTopkLds s_btk;
+    __shared__ AcceptLds acc_lds;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = blockIdx.x;
+    const int64_t r = blockIdx.y;
+    const int k = a.k;
+    const float *row = a.logits + r * a.ld;
+    if (t == 0) s_nan = 0;
+    uint64_t key[kPer];
+    uint32_t my_nan = 0;
+    {
+        float xv[kPer];
+        uint32_t mw[kPer];
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            const int j = min(g * kGroup + p * kTopkThreads + t, a.n_valid - 1);
+            xv[p] = row[j];
+            if constexpr (kMasked) mw[p] = a.mask[r * a.mask_words + (j >> 5)];
+        }
+#pragma unroll
+        for (int p = 0; p < kPer; ++p) {
+            const int j = g * kGroup + p * kTopkThreads + t;
+            key[p] = 0;
+            if (j < a.n_valid) {
+                const float x = xv[p];
+                const bool allowed = !kMasked || ((mw[p] >> (j & 31)) & 1u);
+                if (x != x) my_nan = 1u;
+                else if (allowed) key[p] = cand_key(x, j);
+            }
+        }
+    }
+    __syncthreads();
+    if (my_nan) atomicOr(&s_nan, 1u);
+    const uint64_t best1 = block_topk<kPer>(key, k, s_btk, scratch);
+    if (wave == 0) {
+        const uint64_t best = best1;
+        if (lane < k) store_agent64(a.keys + (r * a.g1 + g) * k + lane, best);
+        if (lane == 0) __hip_atomic_store(a.nan1 + r * a.g1 + g, s_nan, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the wave's stores have reached the shared level
+        if (lane == 0) {
+            const uint32_t c = __hip_atomic_fetch_add(a.count + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = c + 1u == (uint32_t)a.g1;
+        }
+    }
+    __syncthreads();
+    if (!s_last) return;
+
+    // the row's last block: its g1 k keys (at most kGroup), every load out before the first use
+    const int n = a.g1 * k;
+    const uint64_t *rk = a.keys + r * a.g1 * k;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+        const int i = p * kTopkThreads + t;
+        key[p] = load_agent64(rk + min(i, n - 1));
+    }
+    bool f = false;
+    if (wave == 0)
+        for (int c = lane; c < a.g1; c += 64) f |= load_agent32(a.nan1 + r * a.g1 + c) != 0u;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p)
+        if (p * kTopkThreads + t >= n) key[p] = 0;
+    const uint64_t best = block_topk<kPer>(key, k, s_btk, scratch);
+    if (wave != 0) return;
+    const bool any_nan = __ballot(f) != 0;
+    if (lane < k) {
+        const sx_logit_cand c = cand_of(best, row);
+        store_agent64(reinterpret_cast<uint64_t *>(a.cands + r * k + lane),
+                      ((uint64_t)(uint32_t)c.id << 32) | __float_as_uint(c.v));
+    }
+    if (lane == 0) __hip_atomic_store(a.nan + r, any_nan ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int last_row = 0;
+    if (lane == 0) {
+        __hip_atomic_store(a.count + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t c = __hip_atomic_fetch_add(a.count + a.rows, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_row = c + 1u == (uint32_t)a.rows;
+    }
+    if (!__builtin_amdgcn_readfirstlane(last_row)) return;
+    if (lane == 0) __hip_atomic_store(a.count + a.rows, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.out == nullptr) return;  // top-k only
+    const uint64_t *cw = reinterpret_cast<const uint64_t *>(a.cands);
+    accept_walk(
+        [&](int j, int i) {
+            const uint64_t w = load_agent64(cw + (int64_t)j * k + i);
+            sx_logit_cand c;
+            c.v = __uint_as_float((uint32_t)w), c.id = (int32_t)(uint32_t)(w >> 32);
+            return c;
+        },
+        [&](int j) { return load_agent32(a.nan + j); }, k, a.drafts, a.nd, a.u, a.temperature, a.top_k, a.top_p,
+        a.n_valid, a.out, acc_lds);
 }
 
 }  // namespace
@@ -598,6 +874,62 @@ int sx_mtp_pick_ws(const float *logits, int64_t n, const uint32_t *router_err, c
     else
         mtp_pick_ws_kernel<false><<<kPickWsBlocks, kPickWsThreads, 0, s>>>(logits, n, a);
     SX_LAUNCHED("mtp_pick_ws n=", n);
+    return SX_OK;
+}
+
+int sx_verify_tail_workspace_bytes(int64_t rows, int64_t n_valid, int64_t kc, size_t *bytes) {
+    SX_CHECK(bytes != nullptr, "null output");
+    SX_CHECK(rows >= 1 && rows <= 65535 && n_valid >= 1 && kc >= 1 && kc <= 64, "rows = ", rows, ", n_valid = ",
+             n_valid, ", kc = ", kc);
+    const int64_t g1 = groups_of(n_valid);
+    SX_CHECK(g1 * kc <= kGroup, "n_valid = ", n_valid, " at kc = ", kc, " leaves ", g1 * kc,
+             " first-level candidates a row; one launch reduces at most ", kGroup);
+    *bytes = (size_t)(rows * g1 * kc) * 8 + (size_t)(rows * g1) * 4 + (size_t)(rows + 1) * 4;
+    return SX_OK;
+}
+
+int sx_verify_tail(const float *logits, int64_t rows, int64_t ld, int64_t n_valid, int64_t kc, sx_logit_cand *cands,
+                   uint32_t *nan, const uint32_t *mask, int64_t mask_words, const int32_t *drafts, int64_t k,
+                   const double *u, double temperature, int64_t top_k, double top_p, int32_t *out, void *workspace,
+                   size_t workspace_bytes, sx_stream stream) {
+    SX_CHECK(logits && cands && nan && workspace, "null pointer");
+    SX_CHECK(ld >= n_valid, "row stride ld = ", ld, " < n_valid = ", n_valid);
+    size_t need = 0;
+    if (int rc = sx_verify_tail_workspace_bytes(rows, n_valid, kc, &need)) return rc;
+    SX_CHECK(workspace_bytes >= need, "workspace ", workspace_bytes, " bytes, need ", need);
+    SX_CHECK(aligned(workspace, 8) && aligned(cands, 8), "workspace and cands must be 8-byte aligned");
+    if (mask != nullptr) {
+        SX_CHECK(mask_words >= (n_valid + 31) / 32, "mask_words = ", mask_words, " per row covers ", mask_words * 32,
+                 " ids, need ", (n_valid + 31) / 32, " words for n_valid = ", n_valid);
+        SX_CHECK(aligned(mask, 4), "mask must be 4-byte aligned");
+    } else {
+        SX_CHECK(mask_words == 0, "mask_words = ", mask_words, " without a mask (pass 0 when mask is null)");
+    }
+    if (out != nullptr) {  // the acceptance's preconditions (sx_mtp_accept's)
+        SX_CHECK(k >= 0 && k <= 15 && (k == 0 || drafts), "k = ", k, " drafts, expected 0..15 (drafts non-null)");
+        SX_CHECK(rows >= k + 1, "rows = ", rows, ": one candidate row per draft plus the last");
+        SX_CHECK(temperature >= 0 && temperature <= 100, "temperature ", temperature, ", expected 0..100");
+        SX_CHECK(top_p > 0 && top_p <= 1, "top_p ", top_p, ", expected (0, 1]");
+        SX_CHECK(kc >= (n_valid < 20 ? n_valid : 20), "kc = ", kc, " candidates, the sampler needs min(n_valid, 20)");
+        if (temperature > 0) {
+            SX_CHECK(u != nullptr, "sampled acceptance needs the host's uniform draws");
+            SX_CHECK(top_k >= 1 && top_k <= kc, "top_k = ", top_k, " must be 1..", kc);
+        }
+    }
+    const int64_t g1 = groups_of(n_valid);
+    TailArgs a{};
+    a.logits = logits, a.ld = ld, a.n_valid = (int)n_valid, a.g1 = (int)g1, a.k = (int)kc, a.rows = (int)rows;
+    a.mask = mask, a.mask_words = mask_words;
+    a.keys = static_cast<uint64_t *>(workspace);
+    a.nan1 = reinterpret_cast<uint32_t *>(a.keys + rows * g1 * kc);
+    a.count = a.nan1 + rows * g1;
+    a.cands = cands, a.nan = nan;
+    a.drafts = drafts, a.nd = (int)k, a.u = u, a.temperature = temperature, a.top_k = (int)top_k, a.top_p = top_p;
+    a.out = out;
+    const dim3 grid((unsigned)g1, (unsigned)rows);
+    if (mask != nullptr) topk_accept_kernel<true><<<grid, kTopkThreads, 0, stream_of(stream)>>>(a);
+    else topk_accept_kernel<false><<<grid, kTopkThreads, 0, stream_of(stream)>>>(a);
+    SX_LAUNCHED("verify_tail rows=", rows, " n_valid=", n_valid);
     return SX_OK;
 }
 

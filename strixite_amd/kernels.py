@@ -360,6 +360,35 @@ def pick_from_bytes(b):
     return MtpPick.from_buffer_copy(bytes(b.cpu().numpy().tobytes()))
 
 
+def verify_tail_workspace_bytes(rows, n_valid, kc):
+    n = ctypes.c_size_t()
+    check(lib().sx_verify_tail_workspace_bytes(rows, n_valid, kc, ctypes.byref(n)))
+    return n.value
+
+
+def verify_tail_workspace(rows, n_valid, kc, device="cuda"):
+    """A zeroed workspace for verify_tail (one per stream; each launch leaves its counters at zero)."""
+    return torch.zeros(verify_tail_workspace_bytes(rows, n_valid, kc) // 8 + 1, dtype=torch.int64, device=device)
+
+
+def verify_tail(logits, n_valid, kc, ws, drafts=None, u=None, temperature=0.0, top_k=1, top_p=1.0, mask=None,
+                cands=None, nan=None, out=None, stream=None):
+    """logits_topk (kc candidates a row) and, with drafts, mtp_accept in one launch. Returns (cands [rows, kc, 2],
+    nan, out or None)."""
+    rows, ld = logits.shape[0], logits.stride(0)
+    dev = logits.device
+    cands = torch.empty((rows, kc, 2), dtype=torch.int32, device=dev) if cands is None else cands
+    nan = torch.empty(rows, dtype=torch.int32, device=dev) if nan is None else nan
+    k = 0 if drafts is None else drafts.numel()
+    if drafts is not None and out is None:
+        out = torch.full((2 + k + 1,), -1, dtype=torch.int32, device=dev)
+    mw = 0 if mask is None else mask.shape[1]
+    check(lib().sx_verify_tail(_p(logits), rows, ld, n_valid, kc, _p(cands), _p(nan), _p(mask), mw, _p(drafts), k,
+                               _p(u), float(temperature), int(top_k), float(top_p),
+                               _p(out) if drafts is not None else None, _p(ws), ws.numel() * 8, _s(stream)))
+    return cands, nan, out
+
+
 def mtp_accept(cands, nan, drafts, u, temperature, top_k, top_p, n_valid, out=None, stream=None):
     """cands: the raw [k+1, kc, 2] int32 output of logits_topk. Returns the device int32 vector
     [j, status, tokens...]."""

@@ -4,7 +4,7 @@ preallocated device buffers so a forward allocates nothing.
 """
 import torch
 
-from . import MOE_F32
+from . import MOE_F32, SxError
 from . import kernels as kx
 
 
@@ -95,11 +95,22 @@ class VerifyTail:
         self.ws = torch.empty(kx.topk_workspace_bytes(max_rows, n_valid, k_cands) // 8 + 1, dtype=torch.int64,
                               device=dev)
         self.out = torch.empty(2 + max_rows, dtype=torch.int32, device=dev)
+        # top-k and acceptance as one launch where the first level's candidates fit one block a row
+        try:
+            self.tail_ws = kx.verify_tail_workspace(max_rows, n_valid, k_cands, dev)
+        except SxError:  # more first-level candidates a row than one block reduces: two launches
+            self.tail_ws = None
 
     def forward(self, h, drafts, u, temperature, top_k, top_p, stream=None):
         M = h.shape[0]
         kx.linear(h, self.w, out_act=0, y=self.logits[:M], stream=stream)
+        out = self.out[:2 + drafts.numel() + 1]
+        if self.tail_ws is not None and M >= drafts.numel() + 1:
+            kx.verify_tail(self.logits[:M], self.n_valid, self.kc, self.tail_ws, drafts=drafts, u=u,
+                           temperature=temperature, top_k=top_k, top_p=top_p, cands=self.cands[:M],
+                           nan=self.nan[:M], out=out, stream=stream)
+            return out
         kx.logits_topk(self.logits[:M], self.n_valid, self.kc, ws=self.ws, out=self.cands[:M], nan=self.nan[:M],
                        stream=stream)
         return kx.mtp_accept(self.cands[:M], self.nan[:M], drafts, u, temperature, top_k, top_p, self.n_valid,
-                             out=self.out[:2 + drafts.numel() + 1], stream=stream)
+                             out=out, stream=stream)

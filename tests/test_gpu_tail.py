@@ -200,3 +200,57 @@ def test_config5_verify_tail_full_size():
             o = out.cpu().numpy()
             assert (int(o[0]), int(o[1])) == (target, 0), (mode, target)
             assert list(o[2:2 + target + 1]) == seq[:target + 1]
+
+
+def _two_launch_and_fused(L, n_valid, kc, drafts, u, T, top_k, top_p, ws, mask=None):
+    """(cands, nan, out) of logits_topk + mtp_accept and of the one-launch verify_tail on the same device logits."""
+    import torch
+    Ld = util.f32_dev(L)
+    md = None if mask is None else torch.from_numpy(mask.view(np.int32)).cuda()
+    dd = None if drafts is None else torch.from_numpy(np.asarray(drafts, np.int32)).cuda()
+    ud = None if u is None else torch.from_numpy(np.asarray(u, np.float64)).cuda()
+    _, _, nan2, c2 = kx().logits_topk(Ld, n_valid, kc, mask=md)
+    o2 = None
+    if dd is not None:
+        o2 = kx().mtp_accept(c2, nan2, dd, ud, T, top_k, top_p, n_valid)
+    c1, nan1, o1 = kx().verify_tail(Ld, n_valid, kc, ws, drafts=dd, u=ud, temperature=T, top_k=top_k, top_p=top_p,
+                                    mask=md)
+    sync()
+    res2 = (c2.cpu().numpy(), nan2.cpu().numpy(), None if o2 is None else o2.cpu().numpy())
+    res1 = (c1.cpu().numpy(), nan1.cpu().numpy(), None if o1 is None else o1.cpu().numpy())
+    return res2, res1
+
+
+@pytest.mark.parametrize("n,kc", [(151936, 40), (248320, 20), (4097, 40), (300, 20), (1, 20), (40000, 64)])
+def test_verify_tail_one_launch_matches_two(n, kc):
+    """sx_verify_tail (top-k and acceptance in one launch) gives the candidates, NaN flags and accepted tokens of
+    sx_logits_topk + sx_mtp_accept, bit for bit: ties, -0 / +0, a NaN row, greedy and sampled, launches back to back
+    on one workspace (its counters must come back to zero)."""
+    rng = np.random.default_rng(n + kc)
+    rows = 6
+    ws = kx().verify_tail_workspace(rows, n, kc)
+    for trial in range(4):
+        print(f"verify tail: n={n} kc={kc} trial {trial}", flush=True)
+        L = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+        if n > 10:
+            L[0, 5] = L[0, 9] = L[0].max() + 1  # a tie at the top
+            L[2, 3], L[2, 4] = 0.0, -0.0
+            L[2, :3] = -1e30
+        if trial == 2 and n > 50:
+            L[3, 17] = np.nan
+        T, top_k, top_p = ((0.0, kc, 0.95), (0.7, min(40, kc), 0.95), (1.0, min(20, kc), 1.0), (0.3, 5, 0.5))[trial]
+        ref = L.argmax(1) if T == 0 else np.zeros(rows, np.int64)
+        drafts = [int(ref[j]) for j in range(5)] if T == 0 else list(rng.integers(0, n, 5))
+        u = rng.random(rows)
+        (c2, n2, o2), (c1, n1, o1) = _two_launch_and_fused(L, n, kc, drafts, u, T, top_k, top_p, ws)
+        assert np.array_equal(c1, c2), "candidates differ"
+        assert np.array_equal(n1, n2), "NaN flags differ"
+        j = int(o2[0])
+        assert (int(o1[0]), int(o1[1])) == (j, int(o2[1])), (o1[:2], o2[:2])
+        assert np.array_equal(o1[2:2 + j + 1], o2[2:2 + j + 1])
+    # top-k only (no drafts), with an allow-mask
+    bits = (rng.random((rows, (n + 31) // 32, 32)) < 0.3).astype(np.uint64)
+    words = (bits << np.arange(32, dtype=np.uint64)).sum(-1).astype(np.uint32)
+    L = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    (c2, n2, _), (c1, n1, _) = _two_launch_and_fused(L, n, kc, None, None, 0.0, 1, 1.0, ws, mask=words)
+    assert np.array_equal(c1, c2) and np.array_equal(n1, n2)
