@@ -241,8 +241,8 @@ int sx_mtp_pick_ws(const float *logits, int64_t n, const uint32_t *router_err, c
  * serve/sampler.cpp:183-248), as one kernel whose blocks hand over through counters in `workspace`; no reference
  * counterpart as one call. cands / nan: as sx_logits_topk's out / nan (k = kc), for every row. out (nullable: top-k
  * only): as sx_mtp_accept's, for drafts [k] (rows >= k + 1). workspace: sx_verify_tail_workspace_bytes bytes, 8-byte
- * aligned, ZEROED before its first use (it holds counters each launch leaves at zero); one per stream. Shapes whose
- * first level leaves more than 4096 candidates a row are refused (sx_logits_topk takes them). */
+ * aligned, ZEROED before its first use (it holds counters each launch leaves at zero); one per stream. Rows of more
+ * than 262,144 logits are refused (sx_logits_topk takes them). */
 int sx_verify_tail_workspace_bytes(int64_t rows, int64_t n_valid, int64_t kc, size_t *bytes);
 int sx_verify_tail(const float *logits, int64_t rows, int64_t ld, int64_t n_valid, int64_t kc, sx_logit_cand *cands,
                    uint32_t *nan, const uint32_t *mask, int64_t mask_words, const int32_t *drafts, int64_t k,

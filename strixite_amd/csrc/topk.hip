@@ -184,7 +184,8 @@ struct BlockTopkLds {
 // keys in flight (keys are unique: ids differ); the one of rank r < k is the block's r-th best. No sort and no merge.
 // More candidates than LDS holds (heavy ties at T) take the waves' own top-k lists, merged.
 template <int P>
-__device__ uint64_t block_topk(const uint64_t (&key)[P], int k, BlockTopkLds &L, uint64_t (*region)[kScratchB]) {
+__device__ uint64_t block_topk(const uint64_t (&key)[P], int k, BlockTopkLds &L, uint64_t (*region)[kScratchB],
+                               bool any_order = false) {
     constexpr int kCap = kTopkThreadsB * 2;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     uint64_t head = 0;
@@ -241,6 +242,11 @@ __device__ uint64_t block_topk(const uint64_t (&key)[P], int k, BlockTopkLds &L,
         }
         __syncthreads();
         return list;
+    }
+    if (any_order && C <= 64) {  // a superset of the top k, unranked: the candidates themselves (uniform)
+        const uint64_t r = lane < C ? L.cand[lane] : 0;
+        __syncthreads();
+        return r;
     }
     for (int i = t; i < C; i += kTopkThreadsB) {
         const uint64_t x = L.cand[i];
@@ -594,13 +600,15 @@ __global__ void __launch_bounds__(64)
 // same way (a wave's best k of its strided share, four lists merged), writes the candidates and the row's NaN flag,
 // and counts the row done; the last row's block walks the acceptance on one wave, from the candidates as the other
 // blocks stored them. Counters: zero before the first launch, each set back to zero by the block that read it last.
+constexpr int kMaxWalkRows = 16;  // the acceptance's rows: drafts (<= 15) + 1
+
 struct TailArgs {
     const float *logits;
     int64_t ld;
     int n_valid, g1, k, rows;
     const uint32_t *mask;
     int64_t mask_words;
-    uint64_t *keys;    // [rows][g1][k]
+    uint64_t *keys;    // [rows][g1][64]: each first-level block's candidates (a superset of its top k; 0: none)
     uint32_t *nan1;    // [rows][g1]
     uint32_t *count;   // [rows + 1]
     sx_logit_cand *cands;
@@ -647,6 +655,8 @@ __global__ void __launch_bounds__(kTopkThreads) topk_accept_kernel(TailArgs a) {
     __shared__ int s_last;
     __shared__ BlockTopkLds s_btk;
     __shared__ AcceptLds acc_lds;
+    __shared__ uint64_t walk_cands[kMaxWalkRows][64];
+    __shared__ uint32_t walk_nan[64];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = blockIdx.x;
     const int64_t r = blockIdx.y;
     const int k = a.k;
@@ -677,10 +687,9 @@ __global__ void __launch_bounds__(kTopkThreads) topk_accept_kernel(TailArgs a) {
     }
     __syncthreads();
     if (my_nan) atomicOr(&s_nan, 1u);
-    const uint64_t best1 = block_topk<kPer>(key, k, s_btk, scratch);
+    const uint64_t best1 = block_topk<kPer>(key, k, s_btk, scratch, true);
     if (wave == 0) {
-        const uint64_t best = best1;
-        if (lane < k) store_agent64(a.keys + (r * a.g1 + g) * k + lane, best);
+        store_agent64(a.keys + (r * a.g1 + g) * 64 + lane, best1);  // up to 64 keys: a superset of the block's top k
         if (lane == 0) __hip_atomic_store(a.nan1 + r * a.g1 + g, s_nan, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the wave's stores have reached the shared level
         if (lane == 0) {
@@ -692,8 +701,8 @@ __global__ void __launch_bounds__(kTopkThreads) topk_accept_kernel(TailArgs a) {
     if (!s_last) return;
 
     // the row's last block: its g1 k keys (at most kGroup), every load out before the first use
-    const int n = a.g1 * k;
-    const uint64_t *rk = a.keys + r * a.g1 * k;
+    const int n = a.g1 * 64;
+    const uint64_t *rk = a.keys + r * a.g1 * 64;
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
         const int i = p * kTopkThreads + t;
@@ -724,16 +733,27 @@ __global__ void __launch_bounds__(kTopkThreads) topk_accept_kernel(TailArgs a) {
     if (!__builtin_amdgcn_readfirstlane(last_row)) return;
     if (lane == 0) __hip_atomic_store(a.count + a.rows, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (a.out == nullptr) return;  // top-k only
+    // every row's candidates and NaN flag the walk may read, in one round trip (the other rows' blocks stored them)
     const uint64_t *cw = reinterpret_cast<const uint64_t *>(a.cands);
+    const int nr = a.nd + 1;  // <= kMaxWalkRows
+    uint64_t pc[kMaxWalkRows];
+#pragma unroll
+    for (int j = 0; j < kMaxWalkRows; ++j) pc[j] = load_agent64(cw + (int64_t)min(j, nr - 1) * k + min(lane, k - 1));
+    const uint32_t pn = load_agent32(a.nan + min(lane, nr - 1));
+#pragma unroll
+    for (int j = 0; j < kMaxWalkRows; ++j)
+        if (j < nr) walk_cands[j][lane] = pc[j];
+    walk_nan[lane] = pn;
+    wave_sync();
     accept_walk(
         [&](int j, int i) {
-            const uint64_t w = load_agent64(cw + (int64_t)j * k + i);
+            const uint64_t w = walk_cands[j][i];
             sx_logit_cand c;
             c.v = __uint_as_float((uint32_t)w), c.id = (int32_t)(uint32_t)(w >> 32);
             return c;
         },
-        [&](int j) { return load_agent32(a.nan + j); }, k, a.drafts, a.nd, a.u, a.temperature, a.top_k, a.top_p,
-        a.n_valid, a.out, acc_lds);
+        [&](int j) { return walk_nan[j]; }, k, a.drafts, a.nd, a.u, a.temperature, a.top_k, a.top_p, a.n_valid,
+        a.out, acc_lds);
 }
 
 }  // namespace
@@ -882,9 +902,9 @@ int sx_verify_tail_workspace_bytes(int64_t rows, int64_t n_valid, int64_t kc, si
     SX_CHECK(rows >= 1 && rows <= 65535 && n_valid >= 1 && kc >= 1 && kc <= 64, "rows = ", rows, ", n_valid = ",
              n_valid, ", kc = ", kc);
     const int64_t g1 = groups_of(n_valid);
-    SX_CHECK(g1 * kc <= kGroup, "n_valid = ", n_valid, " at kc = ", kc, " leaves ", g1 * kc,
-             " first-level candidates a row; one launch reduces at most ", kGroup);
-    *bytes = (size_t)(rows * g1 * kc) * 8 + (size_t)(rows * g1) * 4 + (size_t)(rows + 1) * 4;
+    SX_CHECK(g1 * 64 <= kGroup, "n_valid = ", n_valid, " leaves ", g1, " first-level groups a row; one launch "
+             "reduces at most ", kGroup / 64);
+    *bytes = (size_t)(rows * g1 * 64) * 8 + (size_t)(rows * g1) * 4 + (size_t)(rows + 1) * 4;
     return SX_OK;
 }
 
@@ -921,7 +941,7 @@ int sx_verify_tail(const float *logits, int64_t rows, int64_t ld, int64_t n_vali
     a.logits = logits, a.ld = ld, a.n_valid = (int)n_valid, a.g1 = (int)g1, a.k = (int)kc, a.rows = (int)rows;
     a.mask = mask, a.mask_words = mask_words;
     a.keys = static_cast<uint64_t *>(workspace);
-    a.nan1 = reinterpret_cast<uint32_t *>(a.keys + rows * g1 * kc);
+    a.nan1 = reinterpret_cast<uint32_t *>(a.keys + rows * g1 * 64);
     a.count = a.nan1 + rows * g1;
     a.cands = cands, a.nan = nan;
     a.drafts = drafts, a.nd = (int)k, a.u = u, a.temperature = temperature, a.top_k = (int)top_k, a.top_p = top_p;
