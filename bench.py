@@ -22,7 +22,7 @@ sys.path.insert(0, ROOT)
 METRIC = "µs/layer for q4 MoE verify at M=6 + achieved HBM GB/s; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
 ROTATE_BYTES = 1_100_000_000  # weight replicas rotated by the dense GEMV lines: > 4x the 256 MB Infinity Cache
-TRAFFIC_JSON = os.path.join("profiles", "hbm_traffic_cfg3.json")
+TRAFFIC_JSON = os.path.join("profiles", "hbm_traffic.json")
 COPY_PROBE_BYTES = 256 << 20  # FP32 elements read and written once by the calibration kernel
 
 
@@ -293,7 +293,7 @@ def cpu_baseline(layer, xs, budget_s, gpu_logits):
             "routing_flips_cpu_vs_gpu_logits": {"tokens": flips, "of": len(xs) * xs[0].shape[0]}}
 
 
-def prefill_layer(steps=20):
+def prefill_layer(steps=20, probe=False):
     """x BF16 [2048, 4096] through the router projection, the Zipf bias, top-10 routing, grouping,
     the grouped gate_up + SwiGLU and down + combine (q4 G = 128 experts, MFMA 64-slot x 128-row tiles)."""
     import torch
@@ -336,6 +336,13 @@ def prefill_layer(steps=20):
             ev[3].record()
             stamps[i] = ev
 
+    if probe:  # two layers for rocprofv3 --pmc: the traffic of each kernel a launch
+        layer(0)
+        layer(1)
+        torch.cuda.synchronize()
+        U = int((torch.bincount(ids.flatten(), minlength=E) > 0).sum())
+        return {"gg_gate_up": U * gu.nbytes() // E + M * d * 2 + M * k * I * 2,
+                "gg_down": U * dn.nbytes() // E + M * k * I * 2 + M * d * 2}
     ms = time_window(layer, min_launches=steps, min_ms=30.0, windows=3)
     layer(0, mark=True)
     torch.cuda.synchronize()
@@ -434,7 +441,7 @@ def ceilings():
             "mfma_bf16_TFLOPs": mfma, "mfma_best_frac": round(max(mfma.values()) / 2500.0, 4)}
 
 
-def verify_tail():
+def verify_tail(probe=False):
     """Config 5: q8 LM head 151936 x 4096 at M = 6 -> top-40 -> sampled acceptance of 5 drafts."""
     import torch
 
@@ -448,6 +455,11 @@ def verify_tail():
     tail = VerifyTail(w, V, 40, 6)
     drafts = torch.randint(0, V, (5,), dtype=torch.int32, device="cuda")
     u = torch.rand(6, dtype=torch.float64, device="cuda")
+    if probe:  # two verify tails for rocprofv3 --pmc
+        for _ in range(2):
+            tail.forward(h, drafts, u, 0.7, 40, 0.95)
+        torch.cuda.synchronize()
+        return {"lm_head": w.nbytes() + h.numel() * 2 + 6 * V * 4}
     ms = time_window(lambda i: tail.forward(h, drafts, u, 0.7, 40, 0.95), min_launches=100, windows=3)
     ms_head = time_window(lambda i: kx.linear(h, w, out_act=0, y=tail.logits[:6]), min_launches=100, windows=3)
     nb = w.nbytes() + h.numel() * 2 + 2 * 6 * V * 4
@@ -520,6 +532,11 @@ def probe():
     torch.cuda.synchronize()
     alg = {"gate_up": sum(gate_up_bytes(U, gu.nbytes() // E, M, d, E, k, I) for U in Us) / R,
            "down": sum(down_bytes(U, dn.nbytes() // E, M, d, k, I) for U in Us) / R}
+    del layer, gu, dn, Wr
+    torch.cuda.empty_cache()
+    alg.update(prefill_layer(probe=True))  # config 4: grouped gate_up, grouped down (+ its partials' reduce)
+    torch.cuda.empty_cache()
+    alg.update(verify_tail(probe=True))  # config 5: the q8 LM head, then top-k + acceptance
     print(json.dumps({"probe": "done", "algorithmic_bytes_per_launch": alg, "distinct_experts": Us}))
 
 
@@ -538,7 +555,10 @@ def pmc_summary(fetch_dir, write_dir):
                 name, v = r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0  # KiB -> bytes
                 if "MulFunctor" in name:
                     copies.append((int(r["Grid_Size"]), v))
-                key = "gate_up" if "gate_up_kernel" in name else "down" if "down_kernel" in name else None
+                key = ("gg_down" if "gg_down_kernel" in name else "gg_gate_up" if "gg_kernel" in name
+                       else "combine_reduce" if "combine_reduce" in name else "lm_head" if "dense_ks_kernel" in name
+                       else "verify_tail" if "topk_accept_kernel" in name else "gate_up" if "gate_up_kernel" in name
+                       else "down" if "down_kernel" in name else None)
                 if key:
                     rows.setdefault(key, []).append(v)
         big = max(g for g, _ in copies)  # the copy probe: the largest multiply launched
@@ -550,7 +570,9 @@ def pmc_summary(fetch_dir, write_dir):
     out = {"copy_probe_bytes": COPY_PROBE_BYTES, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
            "note": "FETCH_SIZE / WRITE_SIZE (KiB a dispatch) times the factor that makes the copy kernel read and "
                    "write exactly copy_probe_bytes"}
-    for k in ("gate_up", "down"):
+    for k in ("gate_up", "down", "gg_gate_up", "gg_down", "combine_reduce", "lm_head", "verify_tail"):
+        if k not in fetch or k not in write:
+            continue
         fb, wb = fetch[k] * f_scale, write[k] * w_scale
         out[k] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "hbm_bytes_per_launch": int(fb + wb),
                   "raw_fetch_kib": round(fetch[k] / 1024, 1), "raw_write_kib": round(write[k] / 1024, 1)}
