@@ -280,15 +280,6 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
         sl0 = p.shared_logit ? p.shared_logit[(int64_t)min(wave, M - 1) * p.shared_ld] : 0.f;
         sl1 = p.shared_logit ? p.shared_logit[(int64_t)min(wave + kWaves, M - 1) * p.shared_ld] : 0.f;
     }
-    uint4 xr[4][4];
-    {
-        const uint16_t *xrow = p.x + (int64_t)min(n16, M - 1) * K + (int64_t)kq * 4 * kSpan + g * 32;
-#pragma unroll
-        for (int so = 0; so < 4; ++so)
-#pragma unroll
-            for (int t = 0; t < 4; ++t) xr[so][t] = *reinterpret_cast<const uint4 *>(xrow + so * kSpan + t * 8);
-    }
-
     // 2. routing, a wave a token (moe_router.hpp:11-23); only block 0 reports errors and writes ids / coef out
     const bool lead = blockIdx.x == 0;
     if (wave < M)
@@ -301,6 +292,17 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     lds_barrier();
     if constexpr (FUSED) {
         if (fs.trace && tid == 0) fs.trace[8] = __builtin_amdgcn_s_memrealtime();
+    }
+    // the activations only now: issued before the routing they queued ahead of the later waves' logits loads (the
+    // waves of one compute unit share its load path), so the tokens routed by waves 4 .. 7 started about 0.9 us
+    // late; they are first used after the weights' first round trip
+    uint4 xr[4][4];
+    {
+        const uint16_t *xrow = p.x + (int64_t)min(n16, M - 1) * K + (int64_t)kq * 4 * kSpan + g * 32;
+#pragma unroll
+        for (int so = 0; so < 4; ++so)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xr[so][t] = *reinterpret_cast<const uint4 *>(xrow + so * kSpan + t * 8);
     }
     build_units(R, emask, tid < S ? R.ids[tid] : 0, S, A, Ew);
     if constexpr (FUSED) {
@@ -617,7 +619,8 @@ __device__ __forceinline__ void down_body(const DownParams &p, DnLds &L, Routes 
         }
     };
     if constexpr (!FUSED) {
-        if (p.plan) {  // gate_up's routing as it stored it: one 16-byte load a thread, no rebuilding
+        if (p.plan) {  // gate_up's routing as it stored it: one 16-byte load a thread, no rebuilding (h issued
+                       // behind it: loading h after the first weight loads measured 0.8 us slower)
             const uint4 r = reinterpret_cast<const uint4 *>(p.plan)[min(tid, kPlanQuads - 1)];
             load_h();
             if (tid < kPlanQuads) reinterpret_cast<uint4 *>(&R)[tid] = r;
