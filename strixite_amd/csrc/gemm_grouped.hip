@@ -234,7 +234,9 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) w[nb] = *reinterpret_cast<const uint2 *>(srow[nb] + k);
     };
-    // the span sums of stage st's 64 rows (K step grp): 4 threads a row, 4 chunks each
+    // the span sums of stage st's 64 rows (K step grp): 4 threads a row, 4 chunks each. The reads are inline asm
+    // ending in lgkmcnt(0): the compiler does not track an asm output as a pending LDS load, so the asm waits for
+    // its own reads (lgkmcnt counts LDS operations; nothing else is outstanding on it here)
     auto sum_rows = [&](int st, int grp) __attribute__((always_inline)) {
         const int r = tid >> 2, qd = tid & 3;
         if (!dma_on) return;  // rows 32..63 of a tile of at most 32 slots
@@ -364,6 +366,18 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     // waits (a __syncthreads() fence would wait for every outstanding load, the next steps' included).
     //   wait: everything issued before the previous step has landed (DMA of step k + 1, codes of step k); barrier:
     //   every wave is done with step k - 1 (stage (k + 3) % 4 is free) and sees the DMA of k + 1 and the sums of k.
+    // How the count is derived (vmcnt counts a wave's vector memory operations and they complete in issue order):
+    //   step j issues, in this order, DMA of step j + 3 (kDmaPerWave, first, in `step`), the codes of step j + 2
+    //   (2 after the first half's MFMAs, 2 after the second's, in `compute`) and, when j % 4 == 3, the scale window
+    //   of steps j + 5 .. j + 8 (2): kDmaPerWave + 4 or + 6 = kLoadsPerStep at most. At the top of step k at most
+    //   kLoadsPerStep may still be outstanding, so all of step k - 2's DMA (issued first in that step) has landed:
+    //   that is stage k + 1, whose rows this step sums; stage k landed a step earlier. What may still be out are
+    //   register loads (codes, windows) of steps k - 2 and k - 1, and the compiler puts its own wait before the
+    //   first use of each of those registers. A wave with no DMA (!dma_on) issues kDmaPerWave fewer a step, hence
+    //   the smaller count; the DMA of other waves is covered by their own wait before the same barrier.
+    // A change to what a step issues, or to the order, changes these counts: re-derive them, and run the
+    // grouped kernels twice on the same inputs (the parity tests do) - a load landing after its use shows up as
+    // run-to-run differences.
     auto step = [&](int k, auto st_tag, auto rs_tag, auto two_tag) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_tag)::value;
         if (dma_on)
@@ -382,6 +396,8 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     for (int s = 0; s < kStages - 1; ++s) issue_x(s, s);
     issue_codes(0, cw[0], 0), issue_codes(0, cw[0], 1), issue_window(0, wcur);
     issue_codes(1, cw[1], 0), issue_codes(1, cw[1], 1), issue_window(4, wnxt);
+    // vmcnt(0): the prologue's DMA (stages 0..2) and register loads (codes of steps 0, 1; windows 0 and 4) have all
+    // landed in this wave; the barrier makes every wave's DMA visible before stage 0 is summed
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the first steps landed everywhere
     sum_rows(0, 0);
     // unrolled by the stage count (a multiple of the ring depth) so that stages and ring slots are constants; one
@@ -400,7 +416,9 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     };
     if (two_tb) run(std::true_type{});
     else run(std::false_type{});
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the block exits
+    // vmcnt(0): the clamped loads past the end (steps nk .. nk + 2, never used) land before the block exits - a DMA
+    // still in flight at exit would write into LDS that the next block on this compute unit may own
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // ---- sum over the spans of (m - 128 s)[row] * sum x[slot], on the MFMA: 16 spans an instruction, both operands
     // split into three BF16 terms (t0 = rne(v), t1 = rne(v - t0), t2 = rne(v - t0 - t1): 24 significant bits, as
@@ -641,7 +659,8 @@ __device__ __forceinline__ void pd_run(const Params &p, const unsigned char *xs,
             }
     };
     for (int c = c0; c < c1; ++c) chunk(c);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the block exits
+    // vmcnt(0): the clamped register loads issued past the last chunk (never used) land before the waves exit
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 __global__ void __launch_bounds__(kPdThreads, 1) gg_down_kernel(Params p) {
