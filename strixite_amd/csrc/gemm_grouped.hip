@@ -109,6 +109,17 @@ __device__ __forceinline__ bf16x8 codes8(uint32_t d0, uint32_t d1) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
+// sum + the 8 BF16 values of a 16-byte chunk, in order, as four dot products with (1, 1): a v_dot2 adds a pair's two
+// exact products to the running FP32 sum (4 ALU operations for the 16 of unpacking to FP32 and adding)
+__device__ __forceinline__ float sum_chunk(const uint4 &c, float sum) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, qmm::detail::dword(c, i)), one, sum, false);
+    return sum;
+}
+
 __device__ __forceinline__ void dma16(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
 }
@@ -252,12 +263,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
                          : "v"(at));
             float sum = 0.f;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                float v[8];
-                qmm::detail::unpack8(raw[i], v);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) sum += v[e];
-            }
+            for (int i = 0; i < 2; ++i) sum = sum_chunk(raw[i], sum);
             sum = qmm::detail::group_sum_c<4>(sum);
             if (qd == 0 && grp < nk) xsum[r * kSumStride + grp] = sum;
             return;
@@ -280,12 +286,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
                      : "v"(at));
         float sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float v[8];
-            qmm::detail::unpack8(raw[i], v);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sum += v[e];
-        }
+        for (int i = 0; i < 4; ++i) sum = sum_chunk(raw[i], sum);
         sum = qmm::detail::group_sum_c<4>(sum);
         if (qd == 0 && grp < nk) xsum[r * kSumStride + grp] = sum;
     };
@@ -434,16 +435,37 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
             t[0][e] = a, t[1][e] = b, t[2][e] = (__bf16)(r1 - (float)b);
         }
     };
-    for (int g0 = 0; g0 < nk; g0 += 16) {
+    // The scales and mins of the lane's spans, every load issued before the first use: 4-byte loads (two spans
+    // each; a row's scales start 8-byte aligned, as ngroups % 4 == 0 and the view is 4-byte aligned), clamped into
+    // the row, the spans past nk zeroed below (nk % 4 == 0, so a pair is wholly in or out).
+    constexpr int kPasses = L::kMaxGroups / 16;  // 16 spans a pass
+    uint32_t sm[kPasses][2][2][4];  // [pass][nb][scale, min][pair]
+#pragma unroll
+    for (int g = 0; g < kPasses; ++g)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int at = min(g * 16 + h * 8 + 2 * i, nk - 2);
+                sm[g][nb][0][i] = *reinterpret_cast<const uint32_t *>(srow[nb] + at);
+                sm[g][nb][1][i] = *reinterpret_cast<const uint32_t *>(mrow[nb] + at);
+            }
+#pragma unroll
+    for (int g = 0; g < kPasses; ++g) {
+        const int g0 = g * 16;
+        if (g0 >= nk) break;
         const int gl = g0 + h * 8;  // this lane's 8 spans
         bf16x8 bt[2][3];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             float cmv[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                cmv[e] = gl + e < nk ? fmaf(-L::kOff, bf16_to_f32(srow[nb][gl + e]), bf16_to_f32(mrow[nb][gl + e]))
-                                     : 0.f;
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t sw = sm[g][nb][0][e / 2], mw = sm[g][nb][1][e / 2];
+                const float sv = __uint_as_float((e & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+                const float mv = __uint_as_float((e & 1) ? (mw & 0xFFFF0000u) : (mw << 16));
+                cmv[e] = gl + e < nk ? fmaf(-L::kOff, sv, mv) : 0.f;
+            }
             split3(cmv, bt[nb]);
         }
 #pragma unroll
