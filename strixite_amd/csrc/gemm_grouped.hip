@@ -66,6 +66,7 @@ struct Params {
     int64_t E;
     int nrb;  // row blocks
     int64_t dense_M;  // > 0: a dense linear (GATHER) over dense_M token rows, tile u = tokens 64 u .. (no workspace)
+    int vec_store;    // BF16 output, output rows a multiple of 8 and y 16-byte aligned: stores staged through LDS
 };
 
 // The 1-D grid in groups of 8 tiles x nrb row blocks, row-block-major inside a group: the row blocks of a tile get
@@ -488,6 +489,44 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     }
 
     // ---- stores: tile (tb, nb), lane value v = slot tb * 32 + 8 (v / 4) + 4 h + v % 4, row j of the tile ----
+    if constexpr (sizeof(TY) == 2 && MODE != qmm::COMBINE) {
+        if (p.vec_store) {
+            // BF16 output through LDS: the wave's 64 slots x kF features go to its own stage array (every wave is
+            // past its K loop and has drained its DMA - vmcnt(0) above - once all pass this barrier), then out
+            // as 16-byte stores of 8 features: a quarter (SwiGLU: an eighth) of the store instructions of one
+            // 2-byte store a value, with no per-value address arithmetic
+            constexpr int kF = MODE == qmm::SWIGLU ? 32 : 64, kRowB = kF * 2, kChunksRow = kF / 8;
+            static_assert(kBM * kRowB <= L::kStageBytes, "a wave's staged outputs fit its stage array");
+            asm volatile("s_barrier" ::: "memory");
+            unsigned char *stg = xs_at(wave);
+            TY *hy = static_cast<TY *>(p.y);
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int r = tb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+                    if constexpr (MODE == qmm::SWIGLU) {
+                        const float gv = as_stored(acc[tb][0][v], hy), uv = as_stored(acc[tb][1][v], hy);
+                        *reinterpret_cast<uint16_t *>(stg + r * kRowB + j * 2) =
+                            (uint16_t)f32_to_bf16(as_stored(silu(gv), hy) * uv);
+                    } else {
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb)
+                            *reinterpret_cast<uint16_t *>(stg + r * kRowB + (nb * 32 + j) * 2) =
+                                (uint16_t)f32_to_bf16(acc[tb][nb][v]);
+                    }
+                }
+            const int64_t fbase = r0 + wave * kF;  // the wave's first output row (feature)
+#pragma unroll
+            for (int i = 0; i < kBM * kChunksRow / 64; ++i) {
+                const int c = lane + 64 * i, r = c / kChunksRow, cc = c % kChunksRow;
+                const int64_t f = fbase + cc * 8;  // Nrows % 8 == 0: a chunk is wholly in or out
+                const uint4 val = *reinterpret_cast<const uint4 *>(stg + r * kRowB + cc * 16);
+                if (r < T && f < Nrows) *reinterpret_cast<uint4 *>(hy + s_out[r] * Nrows + f) = val;
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
@@ -784,6 +823,7 @@ hipError_t launch_dense(const void *x, const sx_qview *w, void *y, int64_t M, in
     p.x = static_cast<const uint16_t *>(x), p.q = static_cast<const uint8_t *>(w->q);
     p.scale = static_cast<const uint16_t *>(w->scale), p.minv = static_cast<const uint16_t *>(w->minv);
     p.y = y, p.ws = nullptr, p.A = 1, p.N = w->N, p.K = w->K, p.E = 1, p.dense_M = M;
+    p.vec_store = out_act == SX_ACT_BF16 && p.N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
     p.nrb = (int)((p.N + kWaves * 64 - 1) / (kWaves * 64));
     const int64_t tiles = (M + kBM - 1) / kBM;
     const dim3 grid((unsigned)((tiles + 7) / 8 * 8 * p.nrb));
@@ -811,6 +851,7 @@ hipError_t launch(int mode, const void *x, const sx_qview *w, void *y, const int
     const int64_t S = M * A;
     const int64_t wtiles = S / kBM + E + 2;  // WTmax: an upper bound of the 64-slot tiles; the rest exit at once
     const int64_t out_rows = mode == qmm::SWIGLU ? p.N / 2 : p.N;
+    p.vec_store = out_act == SX_ACT_BF16 && out_rows % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
     const int64_t per_block = mode == qmm::SWIGLU ? kWaves * 32 : kWaves * 64;
     p.nrb = (int)((out_rows + per_block - 1) / per_block);
     const dim3 grid((unsigned)((wtiles + 7) / 8 * 8 * p.nrb));

@@ -201,3 +201,21 @@ def test_dense_prefill_bench_shape(bits, G):
     fw = orc.QWeight(bits, hw.q.reshape(N, per)[feats].ravel(), hw.scale.reshape(N, groups)[feats].ravel(),
                      hw.minv.reshape(N, groups)[feats].ravel(), len(feats), K, G)
     util.assert_close(yh[:, feats], orc.linear_q(xh, fw), what=f"dense q{bits} (all tokens, 128 features)")
+
+
+@pytest.mark.parametrize("bits,G", [(4, 128), (8, 64)])
+def test_staged_stores_match_direct_stores(bits, G):
+    """The MFMA tiles store BF16 outputs through LDS as 16-byte vectors when y is 16-byte aligned (and the row count a
+    multiple of 8), and one value at a time otherwise: the two store paths write the same bits."""
+    import torch
+    M, N, K = 300, 384, 1024
+    rng = np.random.default_rng(90 + bits)
+    w = kx().QWeight.upload(util.rand_qweight(rng, bits, N, K, G))
+    xd = util.bf16_dev(util.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32)))
+    print(f"staged vs direct stores q{bits}", flush=True)
+    y = kx().linear(xd, w)
+    buf = torch.empty(M * N + 1, dtype=torch.bfloat16, device="cuda")
+    y2 = buf[1:].view(M, N)  # 2 bytes past a 16-byte boundary: the direct path
+    kx().linear(xd, w, y=y2)
+    sync()
+    assert np.array_equal(util.host_bits(y), util.host_bits(y2))
