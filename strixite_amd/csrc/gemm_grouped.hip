@@ -810,6 +810,216 @@ __global__ void __launch_bounds__(kPdThreads, 1) gg_down_kernel(Params p) {
     else two ? pd_run<4, true>(p, xs, xsum, s_out, T, bucket, c0, c1) : pd_run<4, false>(p, xs, xsum, s_out, T, bucket, c0, c1);
 }
 
+// ---------------- dense linear below full width: K split over the block's waves ----------------
+// gg_kernel gives a block 64 tokens x 256 rows and walks the whole K a step at a time behind a block barrier; with
+// few tokens there are few blocks (M = 256, N = 4096: 64 of them, one a CU for a quarter of the chip) and the time is
+// the latency of K / 128 steps, whatever M is. Here a block owns 64 tokens x 64 output rows and its four waves take a
+// quarter of K each (nk / 4 K steps), so the grid is four times larger and every wave's chain four times shorter.
+// A wave loads its step's 64 activation rows into registers with row-contiguous 16-byte loads (kChunks lanes a row),
+// kGsRing - 1 steps ahead, and at the step turns them around through its own LDS stage (gg_kernel's swizzled
+// layout) into MFMA operands; the codes of its weight rows come as gg_kernel's. No DMA and no block barrier in the
+// K loop: every load is an ordinary one, so the compiler's own wait counts stay exact. A lane sums its half of each
+// span from its operand registers (the two halves are added after the loop); the quarter's scales and mins are
+// loaded once, up front. At the end the four waves' FP32 sums meet in LDS and wave w adds, in wave order, and stores
+// tile (tb, nb) = (w / 2, w % 2).
+constexpr int kGsRing = 2;  // register ring: a step's loads are issued two steps ahead
+
+template <typename TY, int BITS>
+__global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
+    using L = Lay<BITS>;
+    constexpr int kSpan = L::kSpan, kKk = L::kKk, kMaxQ = L::kMaxGroups / 4;
+    constexpr int kChunks = L::kChunks, kRowsPerLoad = 64 / kChunks;
+    __shared__ __attribute__((aligned(16))) float red[kWaves][4][16][64];  // [wave][tile][value][lane]
+    __shared__ __attribute__((aligned(L::kStageAlign))) unsigned char stage[kWaves][L::kStageBytes];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int j = lane & 31, h = lane >> 5;
+    const int64_t K = p.K, N = p.N, M = p.dense_M;
+    const int nk = (int)(K / kSpan), nq = nk / 4, q0 = wave * nq;  // this wave's K steps: q0 .. q0 + nq - 1
+    const int nrg = (int)((N + 63) / 64);
+    const int u = (int)(blockIdx.x / nrg), g = (int)(blockIdx.x % nrg);
+    const int64_t t0 = (int64_t)u * kBM, n0 = (int64_t)g * 64;
+    const int T = (int)min((int64_t)kBM, M - t0);
+    // load i of a step: token row kRowsPerLoad i + lane / kChunks (past M: the last token again, never stored),
+    // chunk lane % kChunks; weight rows nb = 0, 1 of the lane (past N: the last row again)
+    const int64_t xrow0 = t0 + lane / kChunks;
+    const uint16_t *xq = p.x + (int64_t)q0 * kSpan + (lane % kChunks) * 8;
+    unsigned char *stg = stage[wave];
+    const int64_t rowbytes = BITS == 4 ? K / 2 : K, ngroups = nk;
+    const uint8_t *qr[2];
+    const uint16_t *sr[2], *mr[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int64_t row = min(n0 + nb * 32 + j, N - 1);
+        qr[nb] = p.q + row * rowbytes + (int64_t)q0 * kSpanBytes + h * 32;
+        sr[nb] = p.scale + row * ngroups + q0;
+        mr[nb] = p.minv + row * ngroups + q0;
+    }
+    // the quarter's scales and mins (BF16 bits; indices clamped into it)
+    uint32_t sq[2][kMaxQ], mq[2][kMaxQ];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int q = 0; q < kMaxQ; ++q) {
+            const int qc = min(q, nq - 1);
+            sq[nb][q] = sr[nb][qc];
+            mq[nb][q] = mr[nb][qc];
+        }
+    static_assert(kGsRing == 2, "two activation slots, as separate arrays (one array of both ends up in scratch)");
+    uint4 xa0[kChunks], xa1[kChunks];  // [load]: activations as loaded, slot 0 and 1
+    uint4 cw[kGsRing][2][2];     // [slot][nb][half]: codes
+    auto issue = [&](int q, int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(xq + min(xrow0 + kRowsPerLoad * i, M - 1) * K +
+                                                             (int64_t)q * kSpan);
+            if (slot == 0) xa0[i] = v;
+            else xa1[i] = v;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+                cw[slot][nb][hf] = *reinterpret_cast<const uint4 *>(qr[nb] + (int64_t)q * kSpanBytes + hf * 16);
+    };
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[tb][nb] = f32x16{};
+    float hs[2][kMaxQ];  // the lane's half-span sums of its two token rows
+#pragma unroll
+    for (int s = 0; s < kGsRing - 1; ++s)
+        if (s < nq) issue(s, s);
+    auto step = [&](auto q_tag) __attribute__((always_inline)) {
+        constexpr int q = decltype(q_tag)::value, slot = q % kGsRing;
+        if (q >= nq) return;  // uniform
+        // the step's rows into the stage (chunk c of row r in slot c ^ swz(r)), then the lane's operands out of it.
+        // One stage a wave: its reads of the step before are done (a wave's LDS operations complete in order).
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int r = kRowsPerLoad * i + lane / kChunks;
+            *reinterpret_cast<uint4 *>(stg + r * L::kRowBytes + (((lane % kChunks) ^ L::swz(r)) * 16)) =
+                slot == 0 ? xa0[i] : xa1[i];
+        }
+        if (q + kGsRing - 1 < nq) issue(q + kGsRing - 1, (q + kGsRing - 1) % kGsRing);
+        // lane (j, h)'s operand of MFMA kk, row tb * 32 + j, read one MFMA step ahead
+        auto frag = [&](int kk, uint4 (&f)[2]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                const int row = tb * 32 + j;
+                f[tb] = *reinterpret_cast<const uint4 *>(stg + row * L::kRowBytes +
+                                                         (((h * (kChunks / 2) + kk) ^ L::swz(row)) * 16));
+            }
+        };
+        uint4 xf[2][2];  // [buffer][tb]
+        frag(0, xf[0]);
+        float hsum[2] = {0.f, 0.f};
+        f32x16 D[2][2];
+#pragma unroll
+        for (int kk = 0; kk < kKk; ++kk) {
+            if (kk + 1 < kKk) frag(kk + 1, xf[(kk + 1) & 1]);
+            const int hf = kk / (kKk / 2), kq = kk % (kKk / 2);
+            bf16x8 bop[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const uint4 &c = cw[slot][nb][hf];
+                if constexpr (BITS == 4) bop[nb] = codes_nat(qmm::detail::dword(c, kq));
+                else bop[nb] = codes8(qmm::detail::dword(c, 2 * kq), qmm::detail::dword(c, 2 * kq + 1));
+            }
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                const bf16x8 a = __builtin_bit_cast(bf16x8, xf[kk & 1][tb]);
+                hsum[tb] = sum_chunk(xf[kk & 1][tb], hsum[tb]);
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    D[tb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bop[nb], kk == 0 ? f32x16{} : D[tb][nb], 0, 0,
+                                                                        0);
+            }
+        }
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) hs[tb][q] = hsum[tb];
+        float s_[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) s_[nb] = __uint_as_float(sq[nb][q] << 16);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) acc[tb][nb][v] = fmaf(s_[nb], D[tb][nb][v], acc[tb][nb][v]);
+    };
+    [&]<int... Qs>(std::integer_sequence<int, Qs...>) {
+        (step(std::integral_constant<int, Qs>{}), ...);
+    }(std::make_integer_sequence<int, kMaxQ>{});
+
+    // (m - kOff s)[row] * sum x[token] over the quarter's spans on the MFMA, as gg_kernel's end (three BF16 terms a
+    // side): lane (j, h) holds token j's sums of spans 8 h .. 8 h + 7 (the two halves of a span added, in the same
+    // order in both lanes) and row j's terms of the same spans
+    static_assert(kMaxQ <= 16, "one 16-span MFMA pass");
+    auto split3 = [](const float (&v)[8], bf16x8 (&t)[3]) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const __bf16 a = (__bf16)v[e];
+            const float r1 = v[e] - (float)a;
+            const __bf16 b = (__bf16)r1;
+            t[0][e] = a, t[1][e] = b, t[2][e] = (__bf16)(r1 - (float)b);
+        }
+    };
+    bf16x8 at[2][3], bt[2][3];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+        float full[kMaxQ];
+#pragma unroll
+        for (int q = 0; q < kMaxQ; ++q) {
+            const float mine = q < nq ? hs[tb][q] : 0.f;
+            full[q] = mine + __shfl_xor(mine, 32);
+        }
+        float xv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float lo = full[e], hi = 8 + e < kMaxQ ? full[min(8 + e, kMaxQ - 1)] : 0.f;
+            xv[e] = h ? hi : lo;
+        }
+        split3(xv, at[tb]);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        float cmv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int qlo = e, qhi = min(8 + e, kMaxQ - 1);
+            const uint32_t sw = h ? sq[nb][qhi] : sq[nb][qlo], mw = h ? mq[nb][qhi] : mq[nb][qlo];
+            const int qq = h * 8 + e;
+            cmv[e] = qq < nq ? fmaf(-L::kOff, __uint_as_float(sw << 16), __uint_as_float(mw << 16)) : 0.f;
+        }
+        split3(cmv, bt[nb]);
+    }
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int pa = 0; pa < 3; ++pa)
+#pragma unroll
+                for (int pb = 0; pb < 3 - pa; ++pb)
+                    acc[tb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(at[tb][pa], bt[nb][pb], acc[tb][nb], 0, 0, 0);
+
+    // ---- the four quarters' sums, added in wave order; wave w stores tile (tb, nb) = (w / 2, w % 2) ----
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[wave][t][v][lane] = acc[t / 2][t % 2][v];
+    __syncthreads();
+    const int tb = wave / 2, nb = wave % 2;
+    const int64_t feat = n0 + nb * 32 + j;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const float y = ((red[0][wave][v][lane] + red[1][wave][v][lane]) + red[2][wave][v][lane]) + red[3][wave][v][lane];
+        const int r = tb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+        if (r < T && feat < N) store_act(static_cast<TY *>(p.y), (t0 + r) * N + feat, y);
+    }
+}
+
 template <int MODE, typename TY, int BITS = 4>
 hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
     hipLaunchKernelGGL((gg_kernel<MODE, TY, BITS>), grid, dim3(kThreads), 0, stream, p);
@@ -826,6 +1036,18 @@ hipError_t launch_dense(const void *x, const sx_qview *w, void *y, int64_t M, in
     p.vec_store = out_act == SX_ACT_BF16 && p.N % 8 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
     p.nrb = (int)((p.N + kWaves * 64 - 1) / (kWaves * 64));
     const int64_t tiles = (M + kBM - 1) / kBM;
+    if (M <= kDenseSplitMaxTokens) {  // K split over each block's waves
+        const dim3 gs_grid((unsigned)(tiles * ((p.N + 63) / 64)));
+        auto gs = [&](auto tag, auto bits) {
+            hipLaunchKernelGGL((gs_kernel<decltype(tag), decltype(bits)::value>), gs_grid, dim3(kThreads), 0, stream, p);
+            return hipGetLastError();
+        };
+        if (w->G == 64)
+            return out_act == SX_ACT_F32 ? gs(float{}, std::integral_constant<int, 8>{})
+                                         : gs(uint16_t{}, std::integral_constant<int, 8>{});
+        return out_act == SX_ACT_F32 ? gs(float{}, std::integral_constant<int, 4>{})
+                                     : gs(uint16_t{}, std::integral_constant<int, 4>{});
+    }
     const dim3 grid((unsigned)((tiles + 7) / 8 * 8 * p.nrb));
     if (w->G == 64)  // q8
         return out_act == SX_ACT_F32 ? go<qmm::GATHER, float, 8>(p, grid, stream)

@@ -9,11 +9,15 @@ namespace sx::gg {
 constexpr int64_t kPrefillMinTokens = 32;
 
 bool eligible(int bits, int64_t G, int64_t K, int act);
-// Tokens from which a dense linear takes the grouped kernel's tiles (launch_dense): below, its few tiles leave the
-// chip idle and qmm's dense mode is faster. 4096 x 4096, qmm against the tiles: q4 37 / 59 us at M = 128, 64 / 59 at
-// 255; q8 68 / 91 at 128, 88 / 92 at 192, 115 / 92 at 255.
-constexpr int64_t kDenseMinTokens = 256, kDenseMinTokensQ8 = 200;
+// Tokens from which a dense linear takes the MFMA tiles (launch_dense): below, qmm's dense mode is faster. 4096 x
+// 4096, qmm against the K-split tiles (gs_kernel): q4 20.2 / 23.0 us at M = 64, 25.2 / 23.1 at 96; q8 23.7 / 29.3 at
+// 32, 34.0 / 29.5 at 64.
+constexpr int64_t kDenseMinTokens = 96, kDenseMinTokensQ8 = 48;
 constexpr int64_t dense_min_tokens(int bits) { return bits == 8 ? kDenseMinTokensQ8 : kDenseMinTokens; }
+// Up to this many tokens launch_dense splits K over each block's waves (gs_kernel): four times the blocks, a quarter
+// of the steps each. 4096 x 4096, gs_kernel against gg_kernel: q4 23.5 / 51.5 us at M = 256, 45.9 / 52.0 at 512,
+// 90.4 / 53.2 at 1024; q8 31.3 / 82.5 at 256, 60.8 / 83.2 at 512, 119.8 / 83.5 at 1024.
+constexpr int64_t kDenseSplitMaxTokens = 512;
 // The dense linears the tiles take: eligible's q4, and q8 (G = 64, K % 256 == 0, K <= 4096, BF16 x).
 bool eligible_dense(int bits, int64_t G, int64_t K, int act);
 // A dense linear at prefill width on the same tiles: y [M, w->N] (BF16 or FP32) = x [M, K] (BF16) . deq(w)^T, tile u

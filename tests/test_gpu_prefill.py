@@ -142,11 +142,15 @@ def test_config4_prefill_layer_full_size():
                                                      (8, 64, orc.BF16, orc.BF16, 300, 1280),
                                                      (8, 64, orc.BF16, orc.BF16, 256, 4352),
                                                      (8, 64, orc.BF16, orc.F32, 200, 768),
-                                                     (4, 128, orc.F32, orc.F32, 2048, 4096)])
+                                                     (4, 128, orc.F32, orc.F32, 2048, 4096),
+                                                     (4, 128, orc.BF16, orc.F32, 130, 1024),
+                                                     (4, 128, orc.BF16, orc.BF16, 512, 4096),
+                                                     (8, 64, orc.BF16, orc.BF16, 100, 2048),
+                                                     (8, 64, orc.BF16, orc.F32, 513, 256)])
 def test_dense_linear_prefill_width(bits, G, act, out_act, M, K):
     """linear_q4 / linear_q8 at prefill width (the route *_wmma callers take; q4 G = 128 and q8 G = 64 with BF16 x on
-    the grouped kernel's MFMA tiles, a partial last tile of tokens and of rows included; K = 4352 past the tiles' limit
-    on qmm) against the oracle."""
+    the MFMA tiles: K split over a block's waves up to 512 tokens, whole K a block above; a partial last tile of tokens
+    and of rows included; K = 4352 past the tiles' limit on qmm) against the oracle."""
     N = 384
     rng = np.random.default_rng(bits * 10 + act)
     w = util.rand_qweight(rng, bits, N, K, G)
