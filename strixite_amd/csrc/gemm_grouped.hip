@@ -418,6 +418,22 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     };
     if (two_tb) run(std::true_type{});
     else run(std::false_type{});
+    // The scales and mins of the lane's spans for the end below, every load issued before the first use and before
+    // the drain (their latency overlaps it): 4-byte loads (two spans each; a row's scales start 8-byte aligned, as
+    // ngroups % 4 == 0 and the view is 4-byte aligned), clamped into the row, the spans past nk zeroed below (nk % 4
+    // == 0, so a pair is wholly in or out).
+    constexpr int kPasses = L::kMaxGroups / 16;  // 16 spans a pass
+    uint32_t sm[kPasses][2][2][4];  // [pass][nb][scale, min][pair]
+#pragma unroll
+    for (int g = 0; g < kPasses; ++g)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int at = min(g * 16 + h * 8 + 2 * i, nk - 2);
+                sm[g][nb][0][i] = *reinterpret_cast<const uint32_t *>(srow[nb] + at);
+                sm[g][nb][1][i] = *reinterpret_cast<const uint32_t *>(mrow[nb] + at);
+            }
     // vmcnt(0): the clamped loads past the end (steps nk .. nk + 2, never used) land before the block exits - a DMA
     // still in flight at exit would write into LDS that the next block on this compute unit may own
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -436,21 +452,6 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
             t[0][e] = a, t[1][e] = b, t[2][e] = (__bf16)(r1 - (float)b);
         }
     };
-    // The scales and mins of the lane's spans, every load issued before the first use: 4-byte loads (two spans
-    // each; a row's scales start 8-byte aligned, as ngroups % 4 == 0 and the view is 4-byte aligned), clamped into
-    // the row, the spans past nk zeroed below (nk % 4 == 0, so a pair is wholly in or out).
-    constexpr int kPasses = L::kMaxGroups / 16;  // 16 spans a pass
-    uint32_t sm[kPasses][2][2][4];  // [pass][nb][scale, min][pair]
-#pragma unroll
-    for (int g = 0; g < kPasses; ++g)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int at = min(g * 16 + h * 8 + 2 * i, nk - 2);
-                sm[g][nb][0][i] = *reinterpret_cast<const uint32_t *>(srow[nb] + at);
-                sm[g][nb][1][i] = *reinterpret_cast<const uint32_t *>(mrow[nb] + at);
-            }
 #pragma unroll
     for (int g = 0; g < kPasses; ++g) {
         const int g0 = g * 16;
@@ -501,7 +502,8 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
             unsigned char *stg = xs_at(wave);
             TY *hy = static_cast<TY *>(p.y);
 #pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
+            for (int tb = 0; tb < 2; ++tb) {
+                if (tb == 1 && !two_tb) break;  // rows 32..63 hold no slot (uniform)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int r = tb * 32 + 8 * (v / 4) + 4 * h + v % 4;
@@ -516,6 +518,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
                                 (uint16_t)f32_to_bf16(acc[tb][nb][v]);
                     }
                 }
+            }
             const int64_t fbase = r0 + wave * kF;  // the wave's first output row (feature)
 #pragma unroll
             for (int i = 0; i < kBM * kChunksRow / 64; ++i) {
