@@ -392,7 +392,8 @@ def extra_configs(out):
 
 def dense_prefill():
     """Dense linears at prefill width (the route linear_q4_wmma / linear_q8_wmma's callers take): 4096 x 4096 at
-    M = 2048, q4 G = 128 and q8 G = 64, BF16 in and out."""
+    M = 2048 (gg_kernel) and M = 256 (K split over a block's waves, gs_kernel), q4 G = 128 and q8 G = 64, BF16 in
+    and out."""
     import torch
 
     from strixite_amd import kernels as kx
@@ -400,12 +401,14 @@ def dense_prefill():
     res = {}
     for bits, G, seed in ((4, 128, 70), (8, 64, 72)):
         w = syn.qweight(bits, 4096, 4096, G, seed=seed)
-        x = syn.activations(2048, 4096, seed=seed + 1)
-        y = torch.empty((2048, 4096), dtype=torch.bfloat16, device="cuda")
-        ms = time_window(lambda i: kx.linear(x, w, y=y), min_launches=20, min_ms=20.0)
-        res[f"prefill_dense_q{bits}_4096x4096_M2048"] = {
-            "us": round(ms * 1e3, 1), "mfma_frac": round(2.0 * 2048 * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
-        del w, x, y
+        for M in (2048, 256):
+            x = syn.activations(M, 4096, seed=seed + 1)
+            y = torch.empty((M, 4096), dtype=torch.bfloat16, device="cuda")
+            ms = time_window(lambda i: kx.linear(x, w, y=y), min_launches=20, min_ms=20.0)
+            res[f"prefill_dense_q{bits}_4096x4096_M{M}"] = {
+                "us": round(ms * 1e3, 1), "mfma_frac": round(2.0 * M * 4096 * 4096 / (ms * 1e-3) / 2.5e15, 4)}
+            del x, y
+        del w
     return res
 
 
