@@ -223,3 +223,17 @@ def test_staged_stores_match_direct_stores(bits, G):
     kx().linear(xd, w, y=y2)
     sync()
     assert np.array_equal(util.host_bits(y), util.host_bits(y2))
+
+
+@pytest.mark.parametrize("bits,G,M,N,K", [(4, 128, 100, 100, 512), (8, 64, 60, 72, 256), (4, 128, 511, 200, 1536),
+                                          (8, 64, 300, 40, 4096)])
+def test_dense_k_split_ragged(bits, G, M, N, K):
+    """The K-split tiles (up to 512 tokens) on ragged shapes: output rows not a multiple of 64, one K step a wave
+    (K = 512 q4, 256 q8), a quarter of K not a multiple of the ring, against the oracle."""
+    rng = np.random.default_rng(M + N + K)
+    w = util.rand_qweight(rng, bits, N, K, G)
+    x = util.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    print(f"dense k-split q{bits} M={M} N={N} K={K}", flush=True)
+    y = kx().linear(util.bf16_dev(x), kx().QWeight.upload(w), out_act=orc.F32)
+    sync()
+    util.assert_close(util.host_bits(y), orc.linear_q(x, w, out_act=orc.F32), what=f"k-split q{bits} M={M} N={N}")
