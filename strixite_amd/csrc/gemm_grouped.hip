@@ -78,7 +78,9 @@ __device__ __forceinline__ int tile_of(unsigned id, int nrb) {
 }
 __device__ __forceinline__ int rowblock_of(unsigned id, int nrb) { return (int)((id % (8u * nrb)) / 8); }
 
-// (a & b) | c in one ALU operation (the compiler splits the pattern into an AND and an OR).
+// (a & b) | c in one ALU operation (the compiler splits the pattern into an AND and an OR). Never on a register a
+// load has just written: the compiler's wait-count pass does not look at an asm statement's operands, so it would
+// not wait for the load (seen as run-to-run differences when an operand came straight from the code loads).
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
     uint32_t d;
     asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));

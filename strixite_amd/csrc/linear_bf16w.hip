@@ -204,7 +204,11 @@ __global__ void __launch_bounds__(256) linear_bf16w_mfma_kernel(const TX *x, con
             for (int pp = 0; pp < NPLANE; ++pp) *reinterpret_cast<bw_bf16x8 *>(&xt[BUF][pp][xs_off]) = pl[pp];
         }
         // the weight operand copied out by asm: the slot's registers are then dead before their reload (an operand
-        // aliasing them would make the loop rotate the ring through copies that wait for every load in flight)
+        // aliasing them would make the loop rotate the ring through copies that wait for every load in flight).
+        // The compiler's wait-count pass does not look at an asm statement's operands, so nothing waits for wb[D]
+        // on the asm's behalf: it has landed because issue() loads the slot's activations after its weights, loads
+        // complete in issue order, and the activations' LDS store above (an ordinary store, waited for by the
+        // compiler, and before the volatile asm) needs them.
         uint4 bw;
         asm volatile("v_mov_b32 %0, %4\n\tv_mov_b32 %1, %5\n\tv_mov_b32 %2, %6\n\tv_mov_b32 %3, %7"
                      : "=v"(bw.x), "=v"(bw.y), "=v"(bw.z), "=v"(bw.w)
