@@ -108,14 +108,16 @@ __global__ void __launch_bounds__(256) linear_f32w_kernel(const TX *x, const flo
 // ---------------- router projection at prefill width (M >= 64, BF16 x): MFMA ----------------
 // Each FP32 weight is the exact sum of three BF16 terms (hi = rne(w), mid = rne(w - hi), lo = rne(w - hi - mid)), so
 // x . W = x . hi + x . mid + x . lo with every product exact in v_mfma_f32_16x16x32_bf16 and FP32 accumulation, as
-// the scalar kernel's. A block owns 64 weight rows x 64 tokens; a wave 16 rows x the 64 tokens (4 MFMA tiles sharing
-// each split weight fragment). The block's 64 activation rows of a K step (4 KB) are loaded once, a 16-byte chunk a
-// thread, and shared through a double-buffered LDS tile (rows 80 bytes apart: the operand reads are free of bank
-// conflicts), so the activations are read once per 64 weight rows rather than once per wave.
+// the scalar kernel's (up to the order of the FP32 additions). A block owns 64 weight rows x 64 tokens and splits K in
+// two halves over its 8 waves; a wave 16 rows x the 64 tokens of its half (4 MFMA tiles sharing each split weight
+// fragment). A half's 64 activation rows of a K step (4 KB) are loaded once, a 16-byte chunk a thread, and shared
+// through a double-buffered LDS tile (rows 80 bytes apart: the operand reads are free of bank conflicts), so the
+// activations are read once per 64 weight rows rather than once per wave. 4096 x 512 at M = 2048: 39 us against 45.6
+// with one wave a SIMD over the whole K (the time is the chain of K steps, nearly the same at M = 128).
 typedef __bf16 pw_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pw_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t pw_u32x4 __attribute__((ext_vector_type(4)));  // a vector, not an aggregate: copies stay in registers
-constexpr int kPwTok = 64, kPwRows = 64, kPwMinTokens = 64;
+constexpr int kPwTok = 64, kPwRows = 64, kPwMinTokens = 64, kPwKs = 1;
 constexpr int kPwLd = 40;  // BF16 a token row of the LDS tile (32 of the step + 8 of padding)
 
 __device__ __forceinline__ void split3(const float4 &a, const float4 &b, pw_bf16x8 &hi, pw_bf16x8 &mid, pw_bf16x8 &lo) {
@@ -130,45 +132,65 @@ __device__ __forceinline__ void split3(const float4 &a, const float4 &b, pw_bf16
     }
 }
 
-__global__ void __launch_bounds__(256) linear_f32w_mfma_kernel(const uint16_t *x, const float *W, float *y, int64_t M,
+// KS K sub-steps of 32 a barrier (a step), kPwDepth steps of loads in flight. The three BF16 terms accumulate in
+// three independent sums (no MFMA waits on the one before it), added once at the end. The block's 8 waves are two
+// halves of K (waves 4..7 the second, from K step ceil(nk / 2)), each with its own activation tiles: two waves a
+// SIMD, so one's split and LDS traffic overlaps the other's MFMAs; the halves' sums meet in LDS at the end and are
+// added first half first.
+template <int KS>
+__global__ void __launch_bounds__(512) linear_f32w_mfma_kernel(const uint16_t *x, const float *W, float *y, int64_t M,
                                                                int64_t N, int64_t K) {
-    __shared__ __attribute__((aligned(16))) uint16_t xt[2][kPwTok * kPwLd];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g = lane >> 4;
+    __shared__ __attribute__((aligned(16))) uint16_t xt[2][2][KS][kPwTok * kPwLd];  // [half][buffer][sub-step]
+    __shared__ __attribute__((aligned(16))) float red[4][16][64];                   // the second half's sums
+    const int tid = threadIdx.x & 255, kh = threadIdx.x >> 8, lane = tid & 63, wave = tid >> 6, n16 = lane & 15,
+              g = lane >> 4;
     const int64_t row = (int64_t)blockIdx.x * kPwRows + wave * 16 + n16, t0 = (int64_t)blockIdx.y * kPwTok;
-    const float *wr = W + min(row, N - 1) * K + g * 8;
-    // this thread's chunk of every step's activation tile: token tid / 4 (clamped), 16 bytes at (tid % 4) * 8
-    const uint16_t *xc = x + min(t0 + tid / 4, M - 1) * K + (tid % 4) * 8;
+    const int nk_all = (int)(K / 32), kbeg = kh ? (nk_all + 1) / 2 : 0;
+    const int nk = kh ? nk_all - kbeg : (nk_all + 1) / 2;  // this half's sub-steps (the second may have one fewer)
+    const int64_t kb = nk > 0 ? (int64_t)kbeg * 32 : 0;  // a half with no steps (K = 32) reads step 0, never used
+    const float *wr = W + min(row, N - 1) * K + kb + g * 8;
+    // this thread's chunk of every sub-step's activation tile: token tid / 4 (clamped), 16 bytes at (tid % 4) * 8
+    const uint16_t *xc = x + min(t0 + tid / 4, M - 1) * K + kb + (tid % 4) * 8;
     const int xs_off = (tid / 4) * kPwLd + (tid % 4) * 8;
-    pw_f32x4 acc[4];
+    auto xt_at = [&](int buf, int q) -> uint16_t * { return xt[kh][buf][q]; };
+    pw_f32x4 acc[3][4];  // [term: lo, mid, hi][token tile]
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) acc[tt] = pw_f32x4{0.f, 0.f, 0.f, 0.f};
-    // kPwDepth K steps of loads in flight: step s + kPwDepth is issued into the slot step s frees (K steps past the
-    // end re-load the last step, never used)
-    constexpr int kPwDepth = 4;
-    const int nk = (int)(K / 32);
-    float4 wb[kPwDepth][2];
-    pw_u32x4 xb[kPwDepth];
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[pl][tt] = pw_f32x4{0.f, 0.f, 0.f, 0.f};
+    // kPwDepth steps of loads in flight: step s + kPwDepth is issued into the slot step s frees (sub-steps past the
+    // end re-load the last one, never used)
+    constexpr int kPwDepth = KS == 1 ? 4 : 2;
+    float4 wb[kPwDepth][KS][2];
+    pw_u32x4 xb[kPwDepth][KS];
     auto issue = [&](int step, int slot) __attribute__((always_inline)) {
-        const int64_t k0 = (int64_t)min(step, nk - 1) * 32;
-        wb[slot][0] = *reinterpret_cast<const float4 *>(wr + k0), wb[slot][1] = *reinterpret_cast<const float4 *>(wr + k0 + 4);
-        xb[slot] = *reinterpret_cast<const pw_u32x4 *>(xc + k0);
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            const int64_t k0 = (int64_t)max(min(step * KS + q, nk - 1), 0) * 32;
+            wb[slot][q][0] = *reinterpret_cast<const float4 *>(wr + k0);
+            wb[slot][q][1] = *reinterpret_cast<const float4 *>(wr + k0 + 4);
+            xb[slot][q] = *reinterpret_cast<const pw_u32x4 *>(xc + k0);
+        }
     };
 #pragma unroll
     for (int d = 0; d < kPwDepth; ++d) {
         issue(d, d);
         __builtin_amdgcn_sched_barrier(0);  // in slot order, as the loop issues them (exact wait counts at its head)
     }
-    // one K step on ring slot D (a constant: the slots stay in registers)
+    // one step on ring slot D (a constant: the slots stay in registers)
     auto step = [&](int s0, auto d_tag) __attribute__((always_inline)) {
         constexpr int D = decltype(d_tag)::value, BUF = D & 1;  // kPwDepth is even: the LDS buffer of step s0 + D
-        // the slot's activation chunk into LDS and its weights split before the slot is reloaded (a value still live
-        // at the reload would make the loop rotate the ring through copies that wait for every load)
-        *reinterpret_cast<pw_u32x4 *>(&xt[BUF][xs_off]) = xb[D];
-        pw_bf16x8 hi, mid, lo;
-        split3(wb[D][0], wb[D][1], hi, mid, lo);
-        // a step past the end (the unrolled loop's last round) multiplies zeros: no branch inside the loop, which
-        // would make the wait-count pass wait for every load in flight at the loop head
-        if (s0 + D >= nk) hi = pw_bf16x8{}, mid = pw_bf16x8{}, lo = pw_bf16x8{};
+        // the slot's activation chunks into LDS and its weights split before the slot is reloaded (a value still
+        // live at the reload would make the loop rotate the ring through copies that wait for every load)
+        pw_bf16x8 hi[KS], mid[KS], lo[KS];
+#pragma unroll
+        for (int q = 0; q < KS; ++q) {
+            *reinterpret_cast<pw_u32x4 *>(xt_at(BUF, q) + xs_off) = xb[D][q];
+            split3(wb[D][q][0], wb[D][q][1], hi[q], mid[q], lo[q]);
+            // a sub-step past the end multiplies zeros: no branch inside the loop, which would make the wait-count
+            // pass wait for every load in flight at the loop head
+            if ((s0 + D) * KS + q >= nk) hi[q] = pw_bf16x8{}, mid[q] = pw_bf16x8{}, lo[q] = pw_bf16x8{};
+        }
         __builtin_amdgcn_sched_barrier(0);  // the reload stays after the last use of the slot
         issue(s0 + D + kPwDepth, D);
         // the tile of this step is complete; the other buffer's reads (the step before) are done. LDS-only fences:
@@ -177,28 +199,44 @@ __global__ void __launch_bounds__(256) linear_f32w_mfma_kernel(const uint16_t *x
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            const pw_bf16x8 A = *reinterpret_cast<const pw_bf16x8 *>(&xt[BUF][(tt * 16 + n16) * kPwLd + g * 8]);
-            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, lo, acc[tt], 0, 0, 0);
-            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, mid, acc[tt], 0, 0, 0);
-            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, hi, acc[tt], 0, 0, 0);
-        }
+        for (int q = 0; q < KS; ++q)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const pw_bf16x8 A = *reinterpret_cast<const pw_bf16x8 *>(xt_at(BUF, q) + (tt * 16 + n16) * kPwLd + g * 8);
+                acc[0][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, lo[q], acc[0][tt], 0, 0, 0);
+                acc[1][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, mid[q], acc[1][tt], 0, 0, 0);
+                acc[2][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, hi[q], acc[2][tt], 0, 0, 0);
+            }
     };
-    static_assert(kPwDepth == 4, "the K loop below is unrolled by four");
-    for (int s0 = 0; s0 < nk; s0 += kPwDepth) {
-        step(s0, std::integral_constant<int, 0>{});
-        step(s0, std::integral_constant<int, 1>{});
-        step(s0, std::integral_constant<int, 2>{});
-        step(s0, std::integral_constant<int, 3>{});
+    const int nsteps = (((nk_all + 1) / 2) + KS - 1) / KS;  // both halves take the same steps (the barriers pair up)
+    if constexpr (kPwDepth == 4) {
+        for (int s0 = 0; s0 < nsteps; s0 += 4) {
+            step(s0, std::integral_constant<int, 0>{});
+            step(s0, std::integral_constant<int, 1>{});
+            step(s0, std::integral_constant<int, 2>{});
+            step(s0, std::integral_constant<int, 3>{});
+        }
+    } else {
+        for (int s0 = 0; s0 < nsteps; s0 += 2) {
+            step(s0, std::integral_constant<int, 0>{});
+            step(s0, std::integral_constant<int, 1>{});
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped loads past the end land before the wave exits
-    if (row >= N) return;
+    if (kh == 1) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[wave][tt * 4 + v][lane] = (acc[0][tt][v] + acc[1][tt][v]) + acc[2][tt][v];
+    }
+    __syncthreads();
+    if (kh == 1 || row >= N) return;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int64_t t = t0 + tt * 16 + 4 * g + v;
-            if (t < M) y[t * N + row] = acc[tt][v];
+            if (t < M) y[t * N + row] = ((acc[0][tt][v] + acc[1][tt][v]) + acc[2][tt][v]) + red[wave][tt * 4 + v][lane];
         }
 }
 
@@ -257,7 +295,7 @@ int sx_linear_f32w(const void *x, const float *W, int64_t N, int64_t K, float *y
     SX_CHECK(apart(y, M * N * 4, x, M * K * act_bytes(act)) && apart(y, M * N * 4, W, N * K * 4), "y overlaps inputs");
     if (act == SX_ACT_BF16 && M >= kPwMinTokens && K % 32 == 0 && aligned(x, 16) && (M + kPwTok - 1) / kPwTok <= 65535) {
         const dim3 g2((unsigned)((N + kPwRows - 1) / kPwRows), (unsigned)((M + kPwTok - 1) / kPwTok));
-        linear_f32w_mfma_kernel<<<g2, 256, 0, stream_of(stream)>>>(static_cast<const uint16_t *>(x), W, y, M, N, K);
+        linear_f32w_mfma_kernel<kPwKs><<<g2, 512, 0, stream_of(stream)>>>(static_cast<const uint16_t *>(x), W, y, M, N, K);
         SX_LAUNCHED("linear_f32w (MFMA) M=", M, " N=", N, " K=", K);
         return SX_OK;
     }
