@@ -487,7 +487,7 @@ __global__ void __launch_bounds__(kPickWsThreads) mtp_pick_ws_kernel(const float
 // LDS of one acceptance walk.
 struct AcceptLds {
     sx_logit_cand cs[64];
-    double probs[64], quot[64], sum;
+    double probs[64], quot[64], pre[64], sum;
     int go;
 };
 
@@ -514,13 +514,18 @@ __device__ void accept_walk(CandAt cand, NanAt nan_of, int kc, const int32_t *dr
         const bool sampled = temperature != 0 && isfinite(cs[0].v);  // uniform
         if (sampled && lane < kk) probs[lane] = exp((double)cs[lane].v / temperature - (double)cs[0].v / temperature);
         wave_sync();
-        if (sampled && top_p < 1) {
+        // pre[i] = probs[0] + .. + probs[i], added in order: the sampler's total (pre[kk - 1]), its kept mass
+        // (pre[keep - 1]) and its draw's running sums are all prefixes of this one sequence, so one sequential pass
+        // gives every one of them bit for bit
+        if (sampled) {
             if (lane == 0) {
-                double sum = 0;
-                for (int i = 0; i < kk; ++i) sum += probs[i];
-                L.sum = sum;
+                double acc = 0;
+                for (int i = 0; i < kk; ++i) acc += probs[i], L.pre[i] = acc;
+                L.sum = acc;
             }
             wave_sync();
+        }
+        if (sampled && top_p < 1) {
             if (lane < kk) quot[lane] = probs[lane] / L.sum;
             wave_sync();
         }
@@ -542,8 +547,6 @@ __device__ void accept_walk(CandAt cand, NanAt nan_of, int kc, const int32_t *dr
             } else if (ok) {
                 ok = isfinite(c[0].v);
                 if (ok) {
-                    double sum = 0;
-                    for (int i = 0; i < kk; ++i) sum += probs[i];
                     int keep = kk;
                     if (top_p < 1) {
                         double acc = 0;
@@ -555,14 +558,11 @@ __device__ void accept_walk(CandAt cand, NanAt nan_of, int kc, const int32_t *dr
                             }
                         }
                     }
-                    double kept = 0;
-                    for (int i = 0; i < keep; ++i) kept += probs[i];
+                    const double kept = L.pre[keep - 1];  // probs[0] + .. + probs[keep - 1] in order
                     const double r = u[j] * kept;
-                    double acc = 0;
                     v = c[keep - 1].id;
-                    for (int i = 0; i < keep; ++i) {
-                        acc += probs[i];
-                        if (r < acc) {
+                    for (int i = 0; i < keep; ++i) {  // the draw's running sum after i + 1 terms is pre[i]
+                        if (r < L.pre[i]) {
                             v = c[i].id;
                             break;
                         }
