@@ -40,14 +40,16 @@ namespace {
 // tile_bucket [Tmax], tile_start [Tmax] (16-slot tiles), wtile_bucket [WTmax], wtile_start [WTmax] (64-slot tiles);
 // Tmax = S / 16 + E + 2, WTmax = S / 64 + E + 2 (a bucket of c slots has ceil(c / R) <= c / R + 1 tiles).
 constexpr int kRouteThreads = 1024;  // one bucket a thread: E <= 1023 experts + the invalid-id bucket
+constexpr int kRouteStage = 32768;   // slots placed in LDS (128 KB) before they go out in order
 
 __global__ void __launch_bounds__(kRouteThreads)
     route_kernel(const int32_t *ids, int S, int E, int Tmax, int WTmax, int32_t *ws, uint32_t *err) {
     __shared__ int cnt[kRouteThreads], cursor[kRouteThreads];
     __shared__ int wtot[kRouteThreads / 64][3];
     __shared__ int first_bad;
+    __shared__ int stage[kRouteStage];
     routing::group_in_block<kRouteThreads>([&](int s) { return ids[s]; }, S, E, Tmax, WTmax, ws, err, cnt, cursor,
-                                           wtot, &first_bad);
+                                           wtot, &first_bad, stage, kRouteStage);
 }
 
 // ---------------- combine reduce ----------------

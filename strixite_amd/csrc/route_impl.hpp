@@ -287,10 +287,12 @@ constexpr int kR = 16, kRW = 64;  // slots a tile (16-row MFMA tiles) and a wide
 // slots [S], tile_bucket / tile_start [Tmax], wtile_bucket / wtile_start [WTmax]. Thread t owns a run of
 // consecutive buckets. Slot order within a bucket follows the atomics; no output depends on it. The first
 // invalid slot in slot order (an atomic minimum, independent of scheduling) goes to err = {1, id, slot}.
-// LDS: cnt, cursor [E + 1], wtot [NT / 64][3], first_bad.
+// LDS: cnt, cursor [E + 1], wtot [NT / 64][3], first_bad; optionally stage [stage_cap]: when S <= stage_cap the
+// slots are placed in LDS and leave in order, a coalesced store for 64 of them (placed straight into the workspace,
+// every slot is a store of its own to a scattered address: 20,480 slots took 18 us in one block, 10.7 staged).
 template <int NT, typename IdAt>
 __device__ void group_in_block(IdAt id_at, int S, int E, int Tmax, int WTmax, int32_t *ws, uint32_t *err, int *cnt,
-                               int *cursor, int (*wtot)[3], int *first_bad) {
+                               int *cursor, int (*wtot)[3], int *first_bad, int *stage = nullptr, int stage_cap = 0) {
     const int t = threadIdx.x;
     for (int b = t; b <= E; b += NT) cnt[b] = 0;
     if (t == 0) *first_bad = INT_MAX;
@@ -336,6 +338,8 @@ __device__ void group_in_block(IdAt id_at, int S, int E, int Tmax, int WTmax, in
         offsets[E + 1] = tot[0];
     }
     __syncthreads();
+    const bool staged = S <= stage_cap;  // uniform
+    int32_t *dst = staged ? stage : slots;
     for (int s0 = t; s0 < S; s0 += NT * kIds) {
         int32_t idv[kIds];
 #pragma unroll
@@ -345,8 +349,12 @@ __device__ void group_in_block(IdAt id_at, int S, int E, int Tmax, int WTmax, in
             const int s = s0 + u * NT;
             if (s >= S) break;
             const int32_t id = idv[u];
-            slots[atomicAdd(&cursor[(id < 0 || id >= E) ? E : id], 1)] = s;
+            dst[atomicAdd(&cursor[(id < 0 || id >= E) ? E : id], 1)] = s;
         }
+    }
+    if (staged) {
+        __syncthreads();
+        for (int i = t; i < S; i += NT) slots[i] = stage[i];
     }
 }
 

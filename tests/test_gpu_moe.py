@@ -61,9 +61,11 @@ def test_router_bf16_logits_shared_slot_and_errors():
 
 # ---------------- grouping ----------------
 
-def test_group_routes_invariants():
+@pytest.mark.parametrize("M,A,E", [(300, 10, 40), (2048, 10, 512), (4000, 10, 512)])
+def test_group_routes_invariants(M, A, E):
+    """Up to 32,768 slots the grouping places them in LDS first and writes them out in order; above, straight into
+    the workspace: both give a valid grouping."""
     rng = np.random.default_rng(3)
-    M, A, E = 300, 10, 40
     ids = rng.integers(0, E, (M, A)).astype(np.int32)
     ids[:, 0] = 7                      # one bucket far over 64 slots
     ids[5, 3], ids[9, 1] = -1, E + 3   # invalid ids: bucket E, first one (slot 53) reported
