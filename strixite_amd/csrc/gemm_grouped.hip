@@ -78,13 +78,12 @@ __device__ __forceinline__ int tile_of(unsigned id, int nrb) {
 }
 __device__ __forceinline__ int rowblock_of(unsigned id, int nrb) { return (int)((id % (8u * nrb)) / 8); }
 
-// (a & b) | c in one ALU operation (the compiler splits the pattern into an AND and an OR). Never on a register a
-// load has just written: the compiler's wait-count pass does not look at an asm statement's operands, so it would
-// not wait for the load (seen as run-to-run differences when an operand came straight from the code loads).
+// (a & b) | c in one ALU operation, v_bitop3_b32 with truth table 0xEA (bit 4 S0 + 2 S1 + S2 of the table is the
+// result for those input bits). Written as (a & b) | c the compiler splits it into an AND and an OR; as an intrinsic
+// (not inline asm) its operands are ordinary uses, which the wait-count pass covers: an asm's are not, and an asm
+// form of this on registers straight from the code loads gave run-to-run differences.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
-    uint32_t d;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0xEA);
 }
 
 // Operand of 8 codes (one dword: the low nibble of byte b is code 2b) in natural order as BF16 128 + code: a byte

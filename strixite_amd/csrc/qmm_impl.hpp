@@ -41,21 +41,11 @@ __device__ __forceinline__ float group_sum(float v, int lanes) {
     return v;
 }
 
-// (a & mask) | (b & ~mask) in one v_bfi_b32: the code nibbles under the BF16 exponent bits of 128. (gfx9 VOP3
-// takes no literal, so the compiler would otherwise split it into an and and an or.) Never on a register a load has
-// just written: the compiler's wait-count pass does not look at an asm statement's operands, so it would not wait
-// for the load.
+// (a & mask) | (b & ~mask) in one ALU operation (v_bitop3_b32, truth table 0xCA: S0 ? S1 : S2 bit by bit): the code
+// nibbles under the BF16 exponent bits of 128. An intrinsic rather than inline asm, so the wait-count pass covers
+// its operands (these often come straight from the code loads; it does not look at an asm statement's operands).
 __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
-    uint32_t r;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
-    return r;
-}
-// bfi on a register straight from a load: `after`, an ordinary instruction's result computed from that register, is
-// an extra (unused) operand, so the asm cannot run before it, and the compiler waits for the load before it.
-__device__ __forceinline__ uint32_t bfi_after(uint32_t mask, uint32_t a, uint32_t b, uint32_t after) {
-    uint32_t r;
-    asm("v_bfi_b32 %0, %1, %2, %3 ; after %4" : "=v"(r) : "s"(mask), "v"(a), "v"(b), "v"(after));
-    return r;
+    return __builtin_amdgcn_bitop3_b32(mask, a, b, 0xCA);
 }
 
 // B operand of MFMA t from a lane's 16 code bytes. q4: dword t's nibbles j = 0..7 (code k0 + j) as BF16 128 + code in
@@ -64,8 +54,8 @@ template <int BITS>
 __device__ __forceinline__ bf16x8 codes_b(const uint4 &w, int t) {
     uint4 v;
     if constexpr (BITS == 4) {
-        const uint32_t d = dword(w, t), d4 = d >> 4;  // d comes straight from the code loads: see bfi_after
-        v.x = bfi_after(0x000F000Fu, d, 0x43004300u, d4);
+        const uint32_t d = dword(w, t), d4 = d >> 4;
+        v.x = bfi(0x000F000Fu, d, 0x43004300u);
         v.y = bfi(0x000F000Fu, d4, 0x43004300u);
         v.z = bfi(0x000F000Fu, d >> 8, 0x43004300u);
         v.w = bfi(0x000F000Fu, d >> 12, 0x43004300u);
