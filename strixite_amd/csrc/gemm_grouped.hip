@@ -1024,6 +1024,277 @@ __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
     }
 }
 
+// ---------------- dense linear at full prefill width: 128 tokens a wave ----------------
+// gg_kernel's wave owns 64 tokens x 64 rows: each dequantized weight fragment feeds two MFMAs, and the step's VALU
+// work (dequant, the per-span fold, the span sums: ~9 operations an MFMA) is about as long as its MFMAs, which the
+// two waves of a SIMD overlap only in part. Here (every tile full: the dense case, M > kDenseSplitMaxTokens) a block
+// of 8 waves owns 128 tokens x 256 rows, one block a compute unit (two waves a SIMD), and a wave owns 128 tokens x
+// 32 rows as 4 MFMA tiles: each weight fragment feeds four MFMAs, so the dequant an MFMA halves (~5.5 VALU operations
+// an MFMA) for twice the activation operand reads from LDS, and one barrier every two K steps (the block's eight
+// waves meet at each). Otherwise gg_kernel's arithmetic (span sums, fold, the end's span term on the MFMA) for every
+// output: the results are the same bits. Used where its grid fills the chip (128-token tiles x 256-row blocks >= the
+// compute units): 4096 x 4096 at M = 2048, q4 81.8 -> 71.5 us, q8 117.9 -> 91.4 us.
+constexpr int kGwThreads = 512, kGwWaves = 8, kGwBM = 128, kGwTB = kGwBM / 32, kGwRows = kGwWaves * 32;
+
+template <int BITS>
+struct LayW {
+    static constexpr int kStageBytes = kGwBM * Lay<BITS>::kRowBytes;  // 32 KB / 16 KB
+    static constexpr int kDmaPerWave = kStageBytes / 1024 / kGwWaves;  // 4 / 2
+};
+
+template <typename TY, int BITS>
+__global__ void __launch_bounds__(kGwThreads, 1) gw_kernel(Params p) {
+    using L = Lay<BITS>;
+    using W = LayW<BITS>;
+    constexpr int kSpan = L::kSpan, kStageBytes = W::kStageBytes, kDmaPerWave = W::kDmaPerWave,
+                  kSumStride = L::kSumStride, kChunks = L::kChunks;
+    __shared__ __attribute__((aligned(L::kStageAlign))) unsigned char x0[kStageBytes], x1[kStageBytes],
+        x2[kStageBytes], x3[kStageBytes];
+    __shared__ __attribute__((aligned(16))) float xsum[kGwBM * kSumStride];  // [token][span]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 31, h = lane >> 5;
+    const int64_t K = p.K, N = p.N, M = p.dense_M;
+    const int64_t t0 = (int64_t)tile_of(blockIdx.x, p.nrb) * kGwBM;
+    if (t0 >= M) return;  // past the tile count: uniform for the block
+    const int T = (int)min((int64_t)kGwBM, M - t0);
+    const int64_t r0 = (int64_t)rowblock_of(blockIdx.x, p.nrb) * kGwRows;
+
+    // this lane's weight row, clamped into the weight (stores are masked)
+    const int64_t rowbytes = BITS == 4 ? K / 2 : K, ngroups = K / kSpan;
+    const int64_t feat = r0 + wave * 32 + j;
+    const int64_t wrow = min(feat, N - 1);
+    const uint8_t *qrow = p.q + wrow * rowbytes + h * 32;
+    const uint16_t *srow = p.scale + wrow * ngroups, *mrow = p.minv + wrow * ngroups;
+    // activation DMA: instruction I covers kDmaRows token rows from kDmaRows I (rows past T: token T - 1 again, never
+    // stored); lane l writes row kDmaRows I + l / kChunks, slot l % kChunks with chunk (l % kChunks) ^ swz(row)
+    constexpr int kDmaRows = 64 / kChunks;
+    const uint16_t *xl[kDmaPerWave];
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) {
+        const int r = kDmaRows * (kDmaPerWave * wave + i) + lane / kChunks;
+        xl[i] = p.x + (t0 + min(r, T - 1)) * K + (((lane % kChunks) ^ L::swz(r)) * 8);
+    }
+    auto xs_at = [&](int st) -> unsigned char * { return st == 0 ? x0 : st == 1 ? x1 : st == 2 ? x2 : x3; };
+    const int nk = (int)(K / kSpan);
+    auto issue_x = [&](int kstep, int st) __attribute__((always_inline)) {
+        const int k = min(kstep, nk - 1);
+#pragma unroll
+        for (int i = 0; i < kDmaPerWave; ++i)
+            dma16(xl[i] + (int64_t)k * kSpan, xs_at(st) + (kDmaPerWave * wave + i) * 1024);
+    };
+    uint4 cw[2][2];      // [ring slot][half of the lane's 32 bytes]
+    uint2 wcur, wnxt;    // the scales of 4 steps
+    auto issue_codes = [&](int kstep, uint4 (&w)[2], int half) {
+        const int k = min(kstep, nk - 1);
+        w[half] = *reinterpret_cast<const uint4 *>(qrow + (int64_t)k * kSpanBytes + half * 16);
+    };
+    auto issue_window = [&](int kstep, uint2 &w) {  // steps kstep .. kstep + 3 (clamped: nk % 4 == 0)
+        w = *reinterpret_cast<const uint2 *>(srow + min(kstep, nk - 4));
+    };
+    // the span sums of stage st's 128 rows (K step grp), gg_kernel's: 4 threads a row, the chunks in chunk order;
+    // the reads in asm ending in lgkmcnt(0) (the step's barrier already covers this stage's DMA)
+    auto sum_rows = [&](int st, int grp) __attribute__((always_inline)) {
+        const int r = tid >> 2, qd = tid & 3;
+        float sum = 0.f;
+        if constexpr (BITS == 8) {
+            const uint32_t at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)(
+                xs_at(st) + r * 128 + (((2 * qd) ^ L::swz(r)) * 16));
+            uint4 raw[2];
+            uint32_t tmp;
+            asm volatile("ds_read_b128 %0, %3\n\t"
+                         "v_xor_b32 %2, 16, %3\n\tds_read_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(raw[0]), "=&v"(raw[1]), "=&v"(tmp)
+                         : "v"(at));
+#pragma unroll
+            for (int i = 0; i < 2; ++i) sum = sum_chunk(raw[i], sum);
+        } else {
+            const uint32_t grp0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)(
+                xs_at(st) + r * 256 + ((qd ^ ((r & 15) >> 2)) * 64));
+            const uint32_t at = grp0 + ((uint32_t)(r & 3) << 4);
+            uint4 raw[4];
+            uint32_t tmp;
+            asm volatile("ds_read_b128 %0, %5\n\t"
+                         "v_xor_b32 %4, 16, %5\n\tds_read_b128 %1, %4\n\t"
+                         "v_xor_b32 %4, 32, %5\n\tds_read_b128 %2, %4\n\t"
+                         "v_xor_b32 %4, 48, %5\n\tds_read_b128 %3, %4\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(raw[0]), "=&v"(raw[1]), "=&v"(raw[2]), "=&v"(raw[3]), "=&v"(tmp)
+                         : "v"(at));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum = sum_chunk(raw[i], sum);
+        }
+        sum = qmm::detail::group_sum_c<4>(sum);
+        if (qd == 0 && grp < nk) xsum[r * kSumStride + grp] = sum;
+    };
+
+    f32x16 acc[kGwTB];
+#pragma unroll
+    for (int tb = 0; tb < kGwTB; ++tb) acc[tb] = f32x16{};
+    // one K step on stage st with ring slot RS; the ring slot is re-loaded (step k + 2) as its codes are used
+    auto compute = [&](int k, int st, auto rs_tag) __attribute__((always_inline)) {
+        constexpr int RS = decltype(rs_tag)::value;
+        const unsigned char *xb = xs_at(st);
+        f32x16 D[kGwTB];
+        bf16x8 aop[2][kGwTB];  // [buffer][tb], one MFMA step ahead
+        auto load_a = [&](int kk, bf16x8 (&a)[kGwTB]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int tb = 0; tb < kGwTB; ++tb) {
+                const int row = tb * 32 + j;
+                a[tb] = *reinterpret_cast<const bf16x8 *>(xb + row * L::kRowBytes +
+                                                          (((h * (kChunks / 2) + kk) ^ L::swz(row)) * 16));
+            }
+        };
+        load_a(0, aop[0]);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+#pragma unroll
+            for (int kq = 0; kq < L::kKk / 2; ++kq) {
+                const int kk = half * (L::kKk / 2) + kq;
+                if (kk < L::kKk - 1) load_a(kk + 1, aop[(kk + 1) & 1]);
+                const uint4 &c = cw[RS][half];
+                bf16x8 bop;
+                if constexpr (BITS == 4) bop = codes_nat(qmm::detail::dword(c, kq));
+                else bop = codes8(qmm::detail::dword(c, 2 * kq), qmm::detail::dword(c, 2 * kq + 1));
+#pragma unroll
+                for (int tb = 0; tb < kGwTB; ++tb)
+                    D[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop[kk & 1][tb], bop, kk == 0 ? f32x16{} : D[tb],
+                                                                    0, 0, 0);
+            }
+            issue_codes(k + 2, cw[RS], half);  // this half's codes are in the operands
+        }
+        const uint32_t wd = (st & 2) ? wcur.y : wcur.x;
+        const float s_ = __uint_as_float((st & 1) ? (wd & 0xFFFF0000u) : (wd << 16));
+        if (st == 3) {  // the next window becomes current (loaded four steps ago); the one after is issued
+            wcur = wnxt;
+            issue_window(k + 5, wnxt);
+        }
+#pragma unroll
+        for (int tb = 0; tb < kGwTB; ++tb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[tb][v] = fmaf(s_, D[tb][v], acc[tb][v]);
+    };
+    // One barrier every two K steps: at the top of an even step k every wave has finished steps k - 2 and k - 1
+    // (their stages are free) and the DMA of steps k and k + 1 (issued at the top of step k - 2) is visible; the DMA of
+    // steps k + 2 and k + 3 goes out into the freed stages. Wait count: after a DMA pair a wave issues the code loads
+    // of two steps (2 each) and at most one scale window (every fourth step) before the next barrier, so with at most
+    // kBetween loads outstanding the pair has landed (vmcnt counts a wave's loads, completed in issue order).
+    constexpr int kBetween = 5;
+    auto step = [&](int k, auto st_tag, auto rs_tag) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_tag)::value;
+        if constexpr (ST % 2 == 0) {
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kBetween) : "memory");
+            issue_x(k + 2, (ST + 2) % kStages);
+            issue_x(k + 3, (ST + 3) % kStages);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        sum_rows(ST, k);
+        compute(k, ST, rs_tag);
+    };
+    issue_x(0, 0), issue_x(1, 1);
+    issue_codes(0, cw[0], 0), issue_codes(0, cw[0], 1), issue_window(0, wcur);
+    issue_codes(1, cw[1], 0), issue_codes(1, cw[1], 1), issue_window(4, wnxt);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    for (int k = 0;; k += kStages) {
+        if (k >= nk) break;
+        step(k, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+        if (k + 1 >= nk) break;
+        step(k + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+        if (k + 2 >= nk) break;
+        step(k + 2, std::integral_constant<int, 2>{}, std::integral_constant<int, 0>{});
+        if (k + 3 >= nk) break;
+        step(k + 3, std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{});
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave's span sums are in LDS
+    // the end's scales and mins (gg_kernel's), then the drain of the clamped loads past the end
+    constexpr int kPasses = L::kMaxGroups / 16;
+    uint32_t sm[kPasses][2][4];  // [pass][scale, min][pair]
+#pragma unroll
+    for (int g = 0; g < kPasses; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int at = min(g * 16 + h * 8 + 2 * i, nk - 2);
+            sm[g][0][i] = *reinterpret_cast<const uint32_t *>(srow + at);
+            sm[g][1][i] = *reinterpret_cast<const uint32_t *>(mrow + at);
+        }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // sum over the spans of (m - off s)[row] * sum x[token] on the MFMA, gg_kernel's three BF16 terms a side
+    auto split3 = [](const float (&v)[8], bf16x8 (&t)[3]) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const __bf16 a = (__bf16)v[e];
+            const float r1 = v[e] - (float)a;
+            const __bf16 b = (__bf16)r1;
+            t[0][e] = a, t[1][e] = b, t[2][e] = (__bf16)(r1 - (float)b);
+        }
+    };
+#pragma unroll
+    for (int g = 0; g < kPasses; ++g) {
+        const int g0 = g * 16;
+        if (g0 >= nk) break;
+        const int gl = g0 + h * 8;
+        bf16x8 bt[3];
+        {
+            float cmv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t sw = sm[g][0][e / 2], mw = sm[g][1][e / 2];
+                const float sv = __uint_as_float((e & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+                const float mv = __uint_as_float((e & 1) ? (mw & 0xFFFF0000u) : (mw << 16));
+                cmv[e] = gl + e < nk ? fmaf(-L::kOff, sv, mv) : 0.f;
+            }
+            split3(cmv, bt);
+        }
+#pragma unroll
+        for (int tb = 0; tb < kGwTB; ++tb) {
+            float xv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[e] = gl + e < nk ? xsum[(tb * 32 + j) * kSumStride + gl + e] : 0.f;
+            bf16x8 at[3];
+            split3(xv, at);
+#pragma unroll
+            for (int pa = 0; pa < 3; ++pa)
+#pragma unroll
+                for (int pb = 0; pb < 3 - pa; ++pb)
+                    acc[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(at[pa], bt[pb], acc[tb], 0, 0, 0);
+        }
+    }
+    // stores: tile tb, lane value v = token tb * 32 + 8 (v / 4) + 4 h + v % 4, row j of the wave's 32
+    if constexpr (sizeof(TY) == 2) {
+        if (p.vec_store) {  // BF16 through LDS (every wave is past its K loop and has drained its DMA: the barrier)
+            constexpr int kRowB = 32 * 2, kChunksRow = 4, kWaveB = kGwBM * kRowB;  // 8 KB a wave
+            static_assert(2 * kWaveB <= kStageBytes, "two waves' staged outputs fit a stage array");
+            asm volatile("s_barrier" ::: "memory");
+            unsigned char *stg = xs_at(wave >> 1) + (wave & 1) * kWaveB;
+#pragma unroll
+            for (int tb = 0; tb < kGwTB; ++tb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int r = tb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+                    *reinterpret_cast<uint16_t *>(stg + r * kRowB + j * 2) = (uint16_t)f32_to_bf16(acc[tb][v]);
+                }
+            const int64_t fbase = r0 + wave * 32;
+            TY *hy = static_cast<TY *>(p.y);
+#pragma unroll
+            for (int i = 0; i < kGwBM * kChunksRow / 64; ++i) {
+                const int c = lane + 64 * i, r = c / kChunksRow, cc = c % kChunksRow;
+                const int64_t f = fbase + cc * 8;  // N % 8 == 0: a chunk is wholly in or out
+                const uint4 val = *reinterpret_cast<const uint4 *>(stg + r * kRowB + cc * 16);
+                if (r < T && f < N) *reinterpret_cast<uint4 *>(hy + (t0 + r) * N + f) = val;
+            }
+            return;
+        }
+    }
+    if (feat >= N) return;
+#pragma unroll
+    for (int tb = 0; tb < kGwTB; ++tb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = tb * 32 + 8 * (v / 4) + 4 * h + v % 4;
+            if (r < T) store_act(static_cast<TY *>(p.y), (t0 + r) * N + feat, acc[tb][v]);
+        }
+}
+
 template <int MODE, typename TY, int BITS = 4>
 hipError_t go(const Params &p, dim3 grid, hipStream_t stream) {
     hipLaunchKernelGGL((gg_kernel<MODE, TY, BITS>), grid, dim3(kThreads), 0, stream, p);
@@ -1051,6 +1322,21 @@ hipError_t launch_dense(const void *x, const sx_qview *w, void *y, int64_t M, in
                                          : gs(uint16_t{}, std::integral_constant<int, 8>{});
         return out_act == SX_ACT_F32 ? gs(float{}, std::integral_constant<int, 4>{})
                                      : gs(uint16_t{}, std::integral_constant<int, 4>{});
+    }
+    const int64_t wt = (M + kGwBM - 1) / kGwBM, nrb_w = (p.N + kGwRows - 1) / kGwRows;
+    if (wt * nrb_w >= device_cus()) {  // 128 tokens a wave where that grid fills the chip
+        p.nrb = (int)nrb_w;
+        const dim3 gw_grid((unsigned)((wt + 7) / 8 * 8 * nrb_w));
+        auto gw = [&](auto tag, auto bits) {
+            hipLaunchKernelGGL((gw_kernel<decltype(tag), decltype(bits)::value>), gw_grid, dim3(kGwThreads), 0, stream,
+                               p);
+            return hipGetLastError();
+        };
+        if (w->G == 64)
+            return out_act == SX_ACT_F32 ? gw(float{}, std::integral_constant<int, 8>{})
+                                         : gw(uint16_t{}, std::integral_constant<int, 8>{});
+        return out_act == SX_ACT_F32 ? gw(float{}, std::integral_constant<int, 4>{})
+                                     : gw(uint16_t{}, std::integral_constant<int, 4>{});
     }
     const dim3 grid((unsigned)((tiles + 7) / 8 * 8 * p.nrb));
     if (w->G == 64)  // q8

@@ -225,6 +225,26 @@ def test_staged_stores_match_direct_stores(bits, G):
     assert np.array_equal(util.host_bits(y), util.host_bits(y2))
 
 
+@pytest.mark.parametrize("bits,G,M,N,K,out_act", [(4, 128, 2048, 4096, 1024, orc.BF16), (8, 64, 2048, 4096, 512, orc.BF16),
+                                                  (4, 128, 2000, 4104, 1024, orc.BF16), (8, 64, 2000, 4104, 512, orc.F32),
+                                                  (4, 128, 2000, 4096, 512, orc.F32)])
+def test_wide_tiles_match_64_token_tiles(bits, G, M, N, K, out_act):
+    """Where its grid fills the chip (here: all M tokens at once) the dense linear takes 128 tokens a wave; each half
+    of the tokens alone takes gg_kernel's 64-token tiles. Both do the same arithmetic for every output: the same bits
+    (a partial last token tile, a partial last row block, BF16 staged and F32 direct stores included)."""
+    import torch
+    rng = np.random.default_rng(M + N + K + bits)
+    w = kx().QWeight.upload(util.rand_qweight(rng, bits, N, K, G))
+    xd = util.bf16_dev(util.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32)))
+    print(f"wide vs 64-token tiles q{bits} M={M} N={N} K={K} out={out_act}", flush=True)
+    y = kx().linear(xd, w, out_act=out_act)
+    h = M // 2
+    y0 = kx().linear(xd[:h].contiguous(), w, out_act=out_act)
+    y1 = kx().linear(xd[h:].contiguous(), w, out_act=out_act)
+    sync()
+    assert np.array_equal(util.host_bits(y), np.concatenate([util.host_bits(y0), util.host_bits(y1)]))
+
+
 @pytest.mark.parametrize("bits,G,M,N,K", [(4, 128, 100, 100, 512), (8, 64, 60, 72, 256), (4, 128, 511, 200, 1536),
                                           (8, 64, 300, 40, 4096)])
 def test_dense_k_split_ragged(bits, G, M, N, K):
