@@ -7,9 +7,9 @@
 // 32-row tiles; SwiGLU: the gate and the up rows of 32 features) as 2 x 2 v_mfma_f32_32x32x16_bf16 tiles, so each
 // activation fragment read from LDS feeds two MFMAs and each weight fragment two. K advances one span (128 codes =
 // one quantization group) a step:
-//   - the block's 64 activation rows of the span arrive by direct global->LDS loads (DMA) into a 4-stage ring,
-//     three steps ahead, each row's sixteen 16-byte chunks XOR-swizzled so that the MFMA operand reads are free of
-//     bank conflicts; the block sums each row's span one step ahead of its use;
+//   - the block's 64 activation rows of the span arrive by direct global->LDS loads (DMA) into a 4-stage ring, two
+//     steps at a time two steps ahead (one block barrier every two steps), each row's sixteen 16-byte chunks
+//     XOR-swizzled so that the MFMA operand reads are free of bank conflicts; the block sums each row's span;
 //   - each lane loads its weight rows' codes (32 bytes a row a span) and scales straight into registers, two steps
 //     ahead, and turns a dword of codes into the BF16 operand (128 + code) with four byte selects and AND-ORs;
 //   - per span: acc[slot][row] += s[row] * D + (m[row] - 128 s[row]) * sum_span x[slot], with D = the span's
@@ -31,8 +31,6 @@ constexpr int kSpan = 128, kSpanBytes = 64;  // q4 codes / bytes a span (= one G
 constexpr int kStages = 4;                   // activation stages in LDS: three in flight while one is read
 constexpr int kStageBytes = kBM * kSpan * 2;  // 16 KB
 constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 16-byte-a-lane DMA instructions a wave a step (4)
-constexpr int kLoadsPerStep = kDmaPerWave + 6;  // most a step issues: + 4 code loads (2 rows x 2 halves)
-                                                // + 2 scale windows (every fourth step)
 constexpr int kMaxGroups = 32;  // K <= 4096: the span sums of every step stay in LDS
 constexpr int kSumStride = kMaxGroups + 4;  // floats a row (16-byte aligned, rows 4 banks apart)
 
@@ -47,7 +45,6 @@ struct Lay {
     static constexpr int kRowBytes = kSpan * 2;
     static constexpr int kStageBytes = kBM * kRowBytes;   // 16 KB / 8 KB
     static constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;  // 4 / 2
-    static constexpr int kLoadsPerStep = kDmaPerWave + 6;
     static constexpr int kMaxGroups = 4096 / kSpan;        // K <= 4096
     static constexpr int kSumStride = kMaxGroups + 4;
     static constexpr int kKk = kSpan / 16;                 // MFMAs (k = 16) a step: 8 / 4
@@ -130,7 +127,7 @@ template <int MODE, typename TY, int BITS>
 __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     using L = Lay<BITS>;
     constexpr int kSpan = L::kSpan, kStageBytes = L::kStageBytes, kDmaPerWave = L::kDmaPerWave,
-                  kLoadsPerStep = L::kLoadsPerStep, kSumStride = L::kSumStride;
+                  kSumStride = L::kSumStride;
     // One array a stage, so that the wait-count pass tells a stage's DMA apart from the others'.
     __shared__ __attribute__((aligned(L::kStageAlign))) unsigned char x0[kStageBytes], x1[kStageBytes],
         x2[kStageBytes], x3[kStageBytes];
@@ -364,45 +361,42 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
         }
     };
 
-    // One K step k (stage k % 4, ring slot k % 2; both constants in the unrolled loop). A step issues kLoadsPerStep
-    // loads (4 DMA, then 8 register loads as the codes and scales are used); barriers are s_barrier with explicit
-    // waits (a __syncthreads() fence would wait for every outstanding load, the next steps' included).
-    //   wait: everything issued before the previous step has landed (DMA of step k + 1, codes of step k); barrier:
-    //   every wave is done with step k - 1 (stage (k + 3) % 4 is free) and sees the DMA of k + 1 and the sums of k.
-    // How the count is derived (vmcnt counts a wave's vector memory operations and they complete in issue order):
-    //   step j issues, in this order, DMA of step j + 3 (kDmaPerWave, first, in `step`), the codes of step j + 2
-    //   (2 after the first half's MFMAs, 2 after the second's, in `compute`) and, when j % 4 == 3, the scale window
-    //   of steps j + 5 .. j + 8 (2): kDmaPerWave + 4 or + 6 = kLoadsPerStep at most. At the top of step k at most
-    //   kLoadsPerStep may still be outstanding, so all of step k - 2's DMA (issued first in that step) has landed:
-    //   that is stage k + 1, whose rows this step sums; stage k landed a step earlier. What may still be out are
-    //   register loads (codes, windows) of steps k - 2 and k - 1, and the compiler puts its own wait before the
-    //   first use of each of those registers. A wave with no DMA (!dma_on) issues kDmaPerWave fewer a step, hence
-    //   the smaller count; the DMA of other waves is covered by their own wait before the same barrier.
+    // One K step k (stage k % 4, ring slot k % 2; both constants in the unrolled loop); one barrier every two steps
+    // (s_barrier with an explicit wait: a __syncthreads() fence would wait for every outstanding load). At the top of
+    // an even step k: every wave is done with steps k - 2 and k - 1 (stages (k + 2) % 4 and (k + 3) % 4 are free and
+    // take the DMA of steps k + 2 and k + 3 now), and the DMA of steps k and k + 1 (issued at the top of step k - 2)
+    // has landed in every wave and is visible. Each step sums its own stage; the sums meet the end after one more
+    // barrier. (A barrier a step, with the DMA three steps ahead, measured 2-3 % slower.)
+    // How the wait count is derived (vmcnt counts a wave's vector memory operations and they complete in issue order):
+    //   after its DMA pair (kDmaPerWave each, first in the even step) a wave issues, up to the next even step, the
+    //   codes of two steps (2 after each half's MFMAs, in `compute`: 8) and at most one scale window pair (steps j
+    //   with j % 4 == 3 issue one: 2), kBetween = 10 loads. With at most kBetween outstanding at the top of step k,
+    //   the pair issued at the top of step k - 2 has landed; what may still be out are register loads, which the
+    //   compiler waits for before their first use. A wave with no DMA (!dma_on) has no pair to wait for; the same
+    //   count only waits for older register loads. The DMA of other waves is covered by their own wait before the
+    //   same barrier.
     // A change to what a step issues, or to the order, changes these counts: re-derive them, and run the
     // grouped kernels twice on the same inputs (the parity tests do) - a load landing after its use shows up as
     // run-to-run differences.
+    constexpr int kBetween = 10;
     auto step = [&](int k, auto st_tag, auto rs_tag, auto two_tag) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_tag)::value;
-        if (dma_on)
-            asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kLoadsPerStep) : "memory");
-        else  // no DMA a step: the same loads are this many fewer issues back
-            asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kLoadsPerStep - kDmaPerWave)
-                         : "memory");
-        issue_x(k + 3, (ST + 3) % kStages);
-        __builtin_amdgcn_sched_barrier(0);
-        sum_rows((ST + 1) % kStages, k + 1);
+        if constexpr (ST % 2 == 0) {
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kBetween) : "memory");
+            issue_x(k + 2, (ST + 2) % kStages);
+            issue_x(k + 3, (ST + 3) % kStages);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        sum_rows(ST, k);
         compute(k, ST, rs_tag, two_tag);
     };
 
-    // prologue: steps 0..2 of activations, 0..1 of weights, and the sums of step 0
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue_x(s, s);
+    // prologue: steps 0 and 1 of activations and of weights; vmcnt(0): all landed in this wave, and the barrier makes
+    // every wave's DMA visible
+    issue_x(0, 0), issue_x(1, 1);
     issue_codes(0, cw[0], 0), issue_codes(0, cw[0], 1), issue_window(0, wcur);
     issue_codes(1, cw[1], 0), issue_codes(1, cw[1], 1), issue_window(4, wnxt);
-    // vmcnt(0): the prologue's DMA (stages 0..2) and register loads (codes of steps 0, 1; windows 0 and 4) have all
-    // landed in this wave; the barrier makes every wave's DMA visible before stage 0 is summed
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // the first steps landed everywhere
-    sum_rows(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     // unrolled by the stage count (a multiple of the ring depth) so that stages and ring slots are constants; one
     // copy for tiles of more than 32 slots and one for the rest (no branch inside the K loop)
     auto run = [&](auto two_tag) __attribute__((always_inline)) {
@@ -419,6 +413,7 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     };
     if (two_tb) run(std::true_type{});
     else run(std::false_type{});
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave's span sums are in LDS
     // The scales and mins of the lane's spans for the end below, every load issued before the first use and before
     // the drain (their latency overlaps it): 4-byte loads (two spans each; a row's scales start 8-byte aligned, as
     // ngroups % 4 == 0 and the view is 4-byte aligned), clamped into the row, the spans past nk zeroed below (nk % 4
@@ -442,8 +437,8 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
     // ---- sum over the spans of (m - 128 s)[row] * sum x[slot], on the MFMA: 16 spans an instruction, both operands
     // split into three BF16 terms (t0 = rne(v), t1 = rne(v - t0), t2 = rne(v - t0 - t1): 24 significant bits, as
     // the FP32 fold this replaces; the term largely cancels s * 128 * sum x inside s * D, so 16 bits would not do).
-    // The six products down to 2^-16 of the whole; the rest (below 2^-24) are dropped. The sums of the last steps
-    // were written before the last step's barrier. ----
+    // The six products down to 2^-16 of the whole; the rest (below 2^-24) are dropped. Every wave's span sums are in
+    // LDS: the barrier after the K loop. ----
     auto split3 = [](const float (&v)[8], bf16x8 (&t)[3]) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
