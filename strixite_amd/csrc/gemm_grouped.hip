@@ -559,7 +559,9 @@ __global__ void __launch_bounds__(kThreads, 2) gg_kernel(Params p) {
 // step): the K loop only reads LDS, so it has no barrier, and four waves a SIMD (a wave's registers fit in 128)
 // hide each other's latencies. The codes and scales of the step two ahead (across chunk ends) and each chunk's
 // scales and mins for the final fold are ordinary loads the compiler waits for. A block takes the chunks
-// [part * n / kPdSplits, (part + 1) * n / kPdSplits) of its tile.
+// [part * n / kPdSplits, (part + 1) * n / kPdSplits) of its tile, handed out to its waves a 32-row slice at a time
+// from an LDS counter (statically, a wave a chunk's slice, the four waves of a SIMD ended far apart: 486 -> 474 us for
+// config 4's down + combine).
 constexpr int kPdThreads = 1024, kPdWaves = 16, kPdMaxSteps = 8;
 constexpr int kPdChunkRows = kPdWaves * 32;
 constexpr int kPdSumStride = kPdMaxSteps + 4;  // floats a row of the span sums
@@ -574,16 +576,22 @@ __device__ __forceinline__ void pin16(f32x16 &a) {
 
 template <int NK, bool TWO>
 __device__ __forceinline__ void pd_run(const Params &p, const unsigned char *xs, const float *xsum,
-                                       const int64_t *s_out, int T, int bucket, int c0, int c1) {
+                                       const int64_t *s_out, int T, int bucket, int c0, int c1, int *slice_ctr) {
     using Win = std::conditional_t<NK == 8, uint4, uint2>;  // a row's NK BF16 scales (or mins)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int j = lane & 31, h = lane >> 5;
     const int64_t N = p.N, rowbytes = p.K / 2;
-    // the lane's weight row of chunk c (past the end: the last chunk again, loaded and never used), clamped into
-    // the expert
-    auto row_of = [&](int c) -> int64_t {
-        c = min(c, c1 - 1);
-        const int64_t n = (int64_t)c * kPdChunkRows + wave * 32 + j;
+    // slice s: rows 32 (s % kPdWaves) .. + 31 of chunk c0 + s / kPdWaves; a wave takes slice `wave` first, then the
+    // next one from the block's counter (the waves of a SIMD do not progress at one rate: handed out statically,
+    // the block's last waves ended long after its first). The lane's weight row of slice s (past the end: the last
+    // slice again, loaded and never used), clamped into the expert:
+    const int nsl = (c1 - c0) * kPdWaves;
+    auto feat_of = [&](int s) -> int64_t {
+        s = min(s, nsl - 1);
+        return (int64_t)(c0 + s / kPdWaves) * kPdChunkRows + (s % kPdWaves) * 32 + j;
+    };
+    auto row_of = [&](int s) -> int64_t {
+        const int64_t n = feat_of(s);
         return (int64_t)bucket * N + (n < N ? n : N - 1);
     };
     uint4 cw[2][2];     // [ring slot][half]: the step's 32 bytes of codes
@@ -602,7 +610,7 @@ __device__ __forceinline__ void pd_run(const Params &p, const unsigned char *xs,
         return __uint_as_float((s & 1) ? (d & 0xFFFF0000u) : (d << 16));
     };
     {
-        const int64_t r0 = row_of(c0);
+        const int64_t r0 = row_of(wave);
         issue(r0, 0, 0, 0), issue(r0, 0, 0, 1), issue(r0, 1, 1, 0), issue(r0, 1, 1, 1);
     }
     // LDS address of the lane's A fragment of MFMA step kk, K step k, half tb: a_base[tb] ^ (kk << 4) plus the
@@ -614,8 +622,8 @@ __device__ __forceinline__ void pd_run(const Params &p, const unsigned char *xs,
         a_base[tb] = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)(
                          xs + row * 256 + (((h * 8) ^ (row & 15)) * 16));
     }
-    auto chunk = [&](int c) __attribute__((always_inline)) {
-        const int64_t rc = row_of(c), rn = row_of(c + 1);
+    auto chunk = [&](int c, int cn) __attribute__((always_inline)) {
+        const int64_t rc = row_of(c), rn = row_of(cn);
         f32x16 acc[2] = {f32x16{}, f32x16{}};
         auto kstep = [&](auto k_tag) __attribute__((always_inline)) {
             constexpr int k = decltype(k_tag)::value, RS = k & 1;
@@ -704,7 +712,7 @@ __device__ __forceinline__ void pd_run(const Params &p, const unsigned char *xs,
         // FP32 partials: lane value v = slot tb * 32 + 8 (v / 4) + 4 h + v % 4, row j of the wave's 32. The slots'
         // output rows are read here, from an address the compiler cannot see is the same every chunk (hoisted out
         // of the chunk loop, the 32 row offsets would hold 64 registers throughout)
-        const int64_t feat = (int64_t)c * kPdChunkRows + wave * 32 + j;
+        const int64_t feat = feat_of(c);
         uint32_t so = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const int64_t *)s_out;
         int Tc = T, hc = h;  // likewise the slot bounds (hoisted: 32 masks in scalar registers)
         asm volatile("" : "+v"(so), "+s"(Tc), "+v"(hc));
@@ -718,7 +726,13 @@ __device__ __forceinline__ void pd_run(const Params &p, const unsigned char *xs,
                 if (r < Tc && feat < N) static_cast<float *>(p.y)[outs[r] * N + feat] = acc[tb][v];
             }
     };
-    for (int c = c0; c < c1; ++c) chunk(c);
+    for (int c = wave; c < nsl;) {  // wave-uniform
+        int cn = 0;
+        if (lane == 0) cn = atomicAdd(slice_ctr, 1);
+        cn = __builtin_amdgcn_readfirstlane(cn);
+        chunk(c, cn);
+        c = cn;
+    }
     // vmcnt(0): the clamped register loads issued past the last chunk (never used) land before the waves exit
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
@@ -727,7 +741,7 @@ __global__ void __launch_bounds__(kPdThreads, 1) gg_down_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) unsigned char xs[kPdMaxSteps * kStageBytes];
     __shared__ __attribute__((aligned(16))) float xsum[kBM * kPdSumStride];  // [slot][span]
     __shared__ int64_t s_xrow[kBM], s_out[kBM];
-    __shared__ int s_T, s_bucket;
+    __shared__ int s_T, s_bucket, s_slice;
     const int tid = threadIdx.x, lane = tid & 63;
     const int64_t K = p.K, N = p.N;
     const int E = (int)p.E, nk = (int)(K / kSpan);
@@ -803,10 +817,11 @@ __global__ void __launch_bounds__(kPdThreads, 1) gg_down_kernel(Params p) {
         sum = qmm::detail::group_sum_c<4>(sum);
         if (qd == 0) xsum[r * kPdSumStride + g] = sum;
     }
+    if (tid == 0) s_slice = kPdWaves;  // the first slices are the waves' own
     __syncthreads();
     const bool two = T > 32;
-    if (nk == 8) two ? pd_run<8, true>(p, xs, xsum, s_out, T, bucket, c0, c1) : pd_run<8, false>(p, xs, xsum, s_out, T, bucket, c0, c1);
-    else two ? pd_run<4, true>(p, xs, xsum, s_out, T, bucket, c0, c1) : pd_run<4, false>(p, xs, xsum, s_out, T, bucket, c0, c1);
+    if (nk == 8) two ? pd_run<8, true>(p, xs, xsum, s_out, T, bucket, c0, c1, &s_slice) : pd_run<8, false>(p, xs, xsum, s_out, T, bucket, c0, c1, &s_slice);
+    else two ? pd_run<4, true>(p, xs, xsum, s_out, T, bucket, c0, c1, &s_slice) : pd_run<4, false>(p, xs, xsum, s_out, T, bucket, c0, c1, &s_slice);
 }
 
 // ---------------- dense linear below full width: K split over the block's waves ----------------
