@@ -227,11 +227,11 @@ def test_staged_stores_match_direct_stores(bits, G):
 
 @pytest.mark.parametrize("bits,G,M,N,K,out_act", [(4, 128, 2048, 4096, 1024, orc.BF16), (8, 64, 2048, 4096, 512, orc.BF16),
                                                   (4, 128, 2000, 4104, 1024, orc.BF16), (8, 64, 2000, 4104, 512, orc.F32),
-                                                  (4, 128, 2000, 4096, 512, orc.F32)])
+                                                  (4, 128, 2000, 4096, 512, orc.F32), (8, 64, 2048, 4100, 512, orc.BF16)])
 def test_wide_tiles_match_64_token_tiles(bits, G, M, N, K, out_act):
     """Where its grid fills the chip (here: all M tokens at once) the dense linear takes 128 tokens a wave; each half
     of the tokens alone takes gg_kernel's 64-token tiles. Both do the same arithmetic for every output: the same bits
-    (a partial last token tile, a partial last row block, BF16 staged and F32 direct stores included)."""
+    (a partial last token tile, a partial last row block, BF16 staged and BF16 / F32 direct stores included)."""
     import torch
     rng = np.random.default_rng(M + N + K + bits)
     w = kx().QWeight.upload(util.rand_qweight(rng, bits, N, K, G))
