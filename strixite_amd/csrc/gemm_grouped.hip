@@ -1037,11 +1037,11 @@ __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
 // ---------------- dense linear at full prefill width: 128 tokens a wave ----------------
 // gg_kernel's wave owns 64 tokens x 64 rows: each dequantized weight fragment feeds two MFMAs, and the step's VALU
 // work (dequant, the per-span fold, the span sums: ~9 operations an MFMA) is about as long as its MFMAs, which the
-// two waves of a SIMD overlap only in part. Here (every tile full: the dense case, M > kDenseSplitMaxTokens) a block
-// of 8 waves owns 128 tokens x 256 rows, one block a compute unit (two waves a SIMD), and a wave owns 128 tokens x
-// 32 rows as 4 MFMA tiles: each weight fragment feeds four MFMAs, so the dequant an MFMA halves (~5.5 VALU operations
-// an MFMA) for twice the activation operand reads from LDS, and one barrier every two K steps (the block's eight
-// waves meet at each). Otherwise gg_kernel's arithmetic (span sums, fold, the end's span term on the MFMA) for every
+// two waves of a SIMD overlap only in part. Here (dense linears above kDenseSplitMaxTokens tokens: every token tile
+// but the last is full) a block of 8 waves owns 128 tokens x 256 rows, one block a compute unit (two waves a SIMD),
+// and a wave owns 128 tokens x 32 rows as 4 MFMA tiles: each weight fragment feeds four MFMAs, so the dequant an
+// MFMA halves (~5.7 VALU operations an MFMA) for twice the activation operand reads from LDS, and one barrier every
+// two K steps (the block's eight waves meet at each). Otherwise gg_kernel's arithmetic (span sums, fold, the end's span term on the MFMA) for every
 // output: the results are the same bits. Used where its grid fills the chip (128-token tiles x 256-row blocks >= the
 // compute units): 4096 x 4096 at M = 2048, q4 81.8 -> 71.5 us, q8 117.9 -> 91.4 us.
 constexpr int kGwThreads = 512, kGwWaves = 8, kGwBM = 128, kGwTB = kGwBM / 32, kGwRows = kGwWaves * 32;
