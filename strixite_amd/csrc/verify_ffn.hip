@@ -329,17 +329,19 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     // item (Q = 8), rounds gr < S0 the items gr G + blk (the grid sweeps the items together), then items q0 + j of the block's part
     // [q0, q1) of the pool [G S0, F): j = r and nq + r for the first two (r: the block's rank among the nq blocks of
     // the part), then the claims in fs.rnd[gr & 3], from 2 nq on
+    // 32-bit arithmetic (F = U T16 <= kMaxSlots I / 16): a 64-bit division by the grid size is a long software
+    // sequence between the expert list and the first weight loads
     const int T16 = (int)((Nrows + 15) / 16);
-    const int64_t F = (int64_t)U * T16;
+    const int F = U * T16;
     const int G = (int)gridDim.x, blk = (int)blockIdx.x;
-    const int S0 = DYN ? (int)(F * kFixedNum / kFixedDen / G) : 0;
-    const int64_t PF = F - (int64_t)G * S0;  // the pool
+    const int S0 = DYN ? F * kFixedNum / kFixedDen / G : 0;
+    const int PF = F - G * S0;  // the pool
     const int qj = queue_of(blk), grp = blk >> 3;
-    const int q0 = (int)(G * S0 + qj * PF / kQueues), q1 = (int)(G * S0 + (qj + 1) * PF / kQueues);
+    const int q0 = G * S0 + qj * PF / kQueues, q1 = G * S0 + (qj + 1) * PF / kQueues;
     int nq = 0;
     for (int g2 = qj; DYN && g2 * 8 < G; g2 += kQueues) nq += min(8, G - 8 * g2);
     const int rank = 8 * (grp / kQueues) + (blk & 7);
-    const int b0 = DYN ? 0 : (int)(blk * F / G), b1 = DYN ? (int)F : (int)((blk + 1) * F / G);
+    const int b0 = DYN ? 0 : (int)((int64_t)blk * F / G), b1 = DYN ? F : (int)((int64_t)(blk + 1) * F / G);
     const int groups = DYN ? 0 : (b1 - b0 + P - 1) / P;  // rounds (block-uniform; static)
     auto pool_item = [&](int gr) -> int {  // DYN, gr >= S0
         const int j = gr - S0;
