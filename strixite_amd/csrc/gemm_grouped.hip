@@ -830,13 +830,12 @@ __global__ void __launch_bounds__(kPdThreads, 1) gg_down_kernel(Params p) {
 // the latency of K / 128 steps, whatever M is. Here a block owns 64 tokens x 64 output rows and its four waves take a
 // quarter of K each (nk / 4 K steps), so the grid is four times larger and every wave's chain four times shorter.
 // A wave loads its step's 64 activation rows into registers with row-contiguous 16-byte loads (kChunks lanes a row),
-// kGsRing - 1 steps ahead, and at the step turns them around through its own LDS stage (gg_kernel's swizzled
+// one step ahead (q8: two), and at the step turns them around through its own LDS stage (gg_kernel's swizzled
 // layout) into MFMA operands; the codes of its weight rows come as gg_kernel's. No DMA and no block barrier in the
 // K loop: every load is an ordinary one, so the compiler's own wait counts stay exact. A lane sums its half of each
 // span from its operand registers (the two halves are added after the loop); the quarter's scales and mins are
 // loaded once, up front. At the end the four waves' FP32 sums meet in LDS and wave w adds, in wave order, and stores
 // tile (tb, nb) = (w / 2, w % 2).
-constexpr int kGsRing = 2;  // activation slots: a step's rows are loaded one step ahead
 
 template <typename TY, int BITS>
 __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
@@ -878,11 +877,12 @@ __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
             sq[nb][q] = sr[nb][qc];
             mq[nb][q] = mr[nb][qc];
         }
-    static_assert(kGsRing == 2, "two activation slots, as separate arrays (one array of both ends up in scratch)");
-    uint4 xa0[kChunks], xa1[kChunks];  // [load]: activations as loaded, slot 0 and 1
-    // code slots: q8 (16 steps a quarter at K = 4096) issues its codes two steps ahead, its activations one (q8 at
-    // M = 256: 31.1 -> 29.7 us; for q4 two code steps ahead measured no better)
-    constexpr int kCR = BITS == 8 ? 3 : 2;
+    // register slots of activations (kXR) and codes (kCR): loaded kXR - 1 / kCR - 1 steps ahead. q8 (16 steps a
+    // quarter at K = 4096, 32 registers a step's activations) takes three of each: M = 256 31.1 -> 28.2 us, M = 128
+    // 29.5 -> 27.1 us (four of each measured no better); q4 (64 registers a step's activations) two, as more
+    // measured no better. Separate arrays: one array of the slots ends up in scratch.
+    constexpr int kXR = BITS == 8 ? 3 : 2, kCR = BITS == 8 ? 3 : 2;
+    uint4 xa0[kChunks], xa1[kChunks], xa2[kChunks];  // [load]: activations as loaded, slots 0..2
     uint4 cw[kCR][2][2];  // [slot][nb][half]: codes
     auto issue = [&](int q, int slot) __attribute__((always_inline)) {
 #pragma unroll
@@ -890,7 +890,8 @@ __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
             const uint4 v = *reinterpret_cast<const uint4 *>(xq + min(xrow0 + kRowsPerLoad * i, M - 1) * K +
                                                              (int64_t)q * kSpan);
             if (slot == 0) xa0[i] = v;
-            else xa1[i] = v;
+            else if (slot == 1) xa1[i] = v;
+            else xa2[i] = v;
         }
     };
     auto issue_c = [&](int q, int slot) __attribute__((always_inline)) {
@@ -910,10 +911,10 @@ __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
     for (int s = 0; s < kCR - 1; ++s)
         if (s < nq) issue_c(s, s);
 #pragma unroll
-    for (int s = 0; s < kGsRing - 1; ++s)
+    for (int s = 0; s < kXR - 1; ++s)
         if (s < nq) issue(s, s);
     auto step = [&](auto q_tag) __attribute__((always_inline)) {
-        constexpr int q = decltype(q_tag)::value, slot = q % kGsRing;
+        constexpr int q = decltype(q_tag)::value, slot = q % kXR;
         if (q >= nq) return;  // uniform
         // the step's rows into the stage (chunk c of row r in slot c ^ swz(r)), then the lane's operands out of it.
         // One stage a wave: its reads of the step before are done (a wave's LDS operations complete in order).
@@ -921,9 +922,9 @@ __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
         for (int i = 0; i < kChunks; ++i) {
             const int r = kRowsPerLoad * i + lane / kChunks;
             *reinterpret_cast<uint4 *>(stg + r * L::kRowBytes + (((lane % kChunks) ^ L::swz(r)) * 16)) =
-                slot == 0 ? xa0[i] : xa1[i];
+                slot == 0 ? xa0[i] : slot == 1 ? xa1[i] : xa2[i];
         }
-        if (q + kGsRing - 1 < nq) issue(q + kGsRing - 1, (q + kGsRing - 1) % kGsRing);
+        if (q + kXR - 1 < nq) issue(q + kXR - 1, (q + kXR - 1) % kXR);
         if (q + kCR - 1 < nq) issue_c(q + kCR - 1, (q + kCR - 1) % kCR);
         // lane (j, h)'s operand of MFMA kk, row tb * 32 + j, read one MFMA step ahead
         auto frag = [&](int kk, uint4 (&f)[2]) __attribute__((always_inline)) {
