@@ -830,7 +830,7 @@ __global__ void __launch_bounds__(kPdThreads, 1) gg_down_kernel(Params p) {
 // the latency of K / 128 steps, whatever M is. Here a block owns 64 tokens x 64 output rows and its four waves take a
 // quarter of K each (nk / 4 K steps), so the grid is four times larger and every wave's chain four times shorter.
 // A wave loads its step's 64 activation rows into registers with row-contiguous 16-byte loads (kChunks lanes a row),
-// one step ahead (q8: two), and at the step turns them around through its own LDS stage (gg_kernel's swizzled
+// two steps ahead, and at the step turns them around through its own LDS stage (gg_kernel's swizzled
 // layout) into MFMA operands; the codes of its weight rows come as gg_kernel's. No DMA and no block barrier in the
 // K loop: every load is an ordinary one, so the compiler's own wait counts stay exact. A lane sums its half of each
 // span from its operand registers (the two halves are added after the loop); the quarter's scales and mins are
@@ -877,11 +877,10 @@ __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
             sq[nb][q] = sr[nb][qc];
             mq[nb][q] = mr[nb][qc];
         }
-    // register slots of activations (kXR) and codes (kCR): loaded kXR - 1 / kCR - 1 steps ahead. q8 (16 steps a
-    // quarter at K = 4096, 32 registers a step's activations) takes three of each: M = 256 31.1 -> 28.2 us, M = 128
-    // 29.5 -> 27.1 us (four of each measured no better); q4 (64 registers a step's activations) two, as more
-    // measured no better. Separate arrays: one array of the slots ends up in scratch.
-    constexpr int kXR = BITS == 8 ? 3 : 2, kCR = BITS == 8 ? 3 : 2;
+    // register slots of activations (kXR) and codes (kCR): loaded two steps ahead (three slots of each; with one wave
+    // a SIMD the registers are there): 4096 x 4096 at M = 256 q4 23.6 -> 22.6 us, q8 31.1 -> 28.2 us against two
+    // slots (four measured no better for q8). Separate arrays: one array of the slots ends up in scratch.
+    constexpr int kXR = 3, kCR = 3;
     uint4 xa0[kChunks], xa1[kChunks], xa2[kChunks];  // [load]: activations as loaded, slots 0..2
     uint4 cw[kCR][2][2];  // [slot][nb][half]: codes
     auto issue = [&](int q, int slot) __attribute__((always_inline)) {
