@@ -64,8 +64,9 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int M = p.M, Q = p.Q, P = kWaves / Q;
-    const int ip = wave / Q, kq = wave % Q;  // tile lane, K slice (spans SPW kq ..)
+    // Q is a power of two (1 .. 8): shifts and masks, not divisions
+    const int M = p.M, Q = p.Q, lg_q = __builtin_ctz((unsigned)Q), P = kWaves >> lg_q;
+    const int ip = wave >> lg_q, kq = wave & (Q - 1);  // tile lane, K slice (spans SPW kq ..)
     const int64_t K = p.K, N = p.N, ldx = K + 8;
     const int nspan = (int)(K / F::kSpanCodes), chunks8 = (int)(K / 8), lg_chunks = __builtin_ctz((unsigned)chunks8);
     const int n16 = lane & 15, g = lane >> 4;
@@ -76,13 +77,15 @@ __global__ void __launch_bounds__(kThreads) dense_ks_kernel(Params p) {
     // this block's tiles tile_of(j), j < ntile, in rounds of P: strided, blk + j G (the grid sweeps the rows
     // together: the q8 LM head 122 -> 119 us), else the run b0 + j (fewer tiles a block: config 2 q8 16.2 against
     // 17.3 us strided)
-    const int64_t T16 = (N + 15) / 16;
-    const int G = (int)gridDim.x, blk = (int)blockIdx.x;
+    // in 32-bit unsigned arithmetic (T16 * G < 2^32: the launch checks it): a 64-bit division by the grid size is a
+    // long scalar sequence ahead of the first loads
+    const unsigned T16 = (unsigned)((N + 15) / 16);
+    const unsigned G = gridDim.x, blk = blockIdx.x;
     const bool strided = p.strided != 0;
     const int b0 = (int)(blk * T16 / G);
     const int ntile = strided ? (blk < T16 ? (int)((T16 - 1 - blk) / G + 1) : 0) : (int)((blk + 1) * T16 / G) - b0;
-    const int groups = (ntile + P - 1) / P;
-    auto tile_of = [&](int j) { return strided ? j * G + blk : b0 + j; };
+    const int groups = (ntile + P - 1) >> (3 - lg_q);
+    auto tile_of = [&](int j) { return strided ? j * (int)G + (int)blk : b0 + j; };
 
     // weight ring: round r = the slice kq of tile tile_of(r P + ip) (clamped into the block's tiles: a clamped round
     // loads a valid tile and stores nothing); the round's scales / mins as one window of SPW BF16 a row
@@ -296,7 +299,8 @@ size_t lds_bytes(int act, int64_t M, int64_t K, int bits, int64_t G) {
 }
 
 bool eligible(int bits, int64_t G, int64_t N, int64_t K, int64_t M, int act, int out_act, int cus) {
-    (void)N, (void)cus;  // any number of tiles: a block takes a run of them
+    // any number of tiles: a block takes a run of them (its range computed in 32 bits: tiles x blocks < 2^32)
+    if (N < 1 || (N + 15) / 16 * (int64_t)(cus > 0 ? cus : 1) >= (int64_t(1) << 32)) return false;
     if (!((bits == 4 && (G == 128 || G == 64)) || (bits == 8 && G == 64))) return false;
     const int64_t span = bits == 4 ? 128 : 64;
     if (K % span != 0) return false;

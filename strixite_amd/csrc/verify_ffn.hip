@@ -341,7 +341,7 @@ __device__ __forceinline__ void gate_up_body(const GateUpParams &p, GuLds &L, Ro
     int nq = 0;
     for (int g2 = qj; DYN && g2 * 8 < G; g2 += kQueues) nq += min(8, G - 8 * g2);
     const int rank = 8 * (grp / kQueues) + (blk & 7);
-    const int b0 = DYN ? 0 : (int)((int64_t)blk * F / G), b1 = DYN ? F : (int)((int64_t)(blk + 1) * F / G);
+    const int b0 = DYN ? 0 : (int)((unsigned)blk * F / G), b1 = DYN ? F : (int)((unsigned)(blk + 1) * F / G);
     const int groups = DYN ? 0 : (b1 - b0 + P - 1) / P;  // rounds (block-uniform; static)
     auto pool_item = [&](int gr) -> int {  // DYN, gr >= S0
         const int j = gr - S0;
@@ -968,7 +968,8 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerParams lp) {
     // phase A: the router projection, rows [a R / PA, (a + 1) R / PA) for a = b, b + G, ... (at most kProjRows each)
     const int rows = lp.rows, PA = max(G, (rows + kProjRows - 1) / kProjRows);
     for (int a = b; a < PA; a += G) {
-        const int r0 = (int)((int64_t)a * rows / PA), r1 = (int)((int64_t)(a + 1) * rows / PA);
+        // 32-bit unsigned (PA * rows < 2^21): a 64-bit division is a long scalar sequence ahead of the first loads
+        const int r0 = (int)((unsigned)a * rows / PA), r1 = (int)((unsigned)(a + 1) * rows / PA);
         if (r1 > r0) project_item<TW, MT>(lp, pool.proj, r0, r1 - r0);
     }
     stamp(1);
