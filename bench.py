@@ -43,6 +43,8 @@ def parse():
                     help="only the MTP draft head (for rocprofv3 runs): one JSON line with its timings")
     ap.add_argument("--dense-only", action="store_true",
                     help="only the dense prefill-width linears (for rocprofv3 runs): one JSON line with their timings")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only configs 1 and 2, the dense verify-width GEMVs (for rocprofv3 runs): one JSON line")
     ap.add_argument("--tail-only", action="store_true",
                     help="only config 5's verify tail (for rocprofv3 runs): one JSON line with its timings")
     ap.add_argument("--ceilings-only", action="store_true",
@@ -359,15 +361,15 @@ def prefill_layer(steps=20, probe=False):
             "distinct_experts": U, "max_bucket": int(counts.max()), "flops": flops}
 
 
-def extra_configs(out):
+def verify_gemv():
+    """Configs 1 and 2: dense q4 / q8 GEMV over weight replicas rotated launch by launch, more than 1.1 GB of them
+    (4x the 256 MB Infinity Cache), so every launch reads its weights from HBM."""
     import torch
 
     from strixite_amd import kernels as kx
     from strixite_amd import synthetic as syn
 
     res = {}
-    # configs 1 and 2: dense q4 / q8 GEMV over weight replicas rotated launch by launch, more than 1.1 GB of them
-    # (4x the 256 MB Infinity Cache), so every launch reads its weights from HBM
     for name, bits, N, K, G, M, act in (("cfg1_q4_4096x4096_M1_f32", 4, 4096, 4096, 128, 1, torch.float32),
                                         ("cfg2_q4_12288x4096_M6", 4, 12288, 4096, 128, 6, torch.bfloat16),
                                         ("cfg2_q8_12288x4096_M6", 8, 12288, 4096, 64, 6, torch.bfloat16)):
@@ -381,6 +383,11 @@ def extra_configs(out):
                      "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "rotated_MB": round(len(reps) * reps[0].nbytes() / 1e6)}
         del reps
+    return res
+
+
+def extra_configs(out):
+    res = verify_gemv()
     # config 4: the MoE layer at prefill width, M = 2048, Zipf-skewed routing; grouped MFMA experts
     res.update(dense_prefill())
     res["cfg4_prefill_layer"] = prefill_layer()
@@ -612,6 +619,9 @@ def main():
         return
     if args.dense_only:
         print(json.dumps(dense_prefill()))
+        return
+    if args.gemv_only:
+        print(json.dumps(verify_gemv()))
         return
     if args.ceilings_only:
         print(json.dumps({"ceilings": ceilings()}))
