@@ -877,10 +877,11 @@ __global__ void __launch_bounds__(kThreads, 1) gs_kernel(Params p) {
             sq[nb][q] = sr[nb][qc];
             mq[nb][q] = mr[nb][qc];
         }
-    // register slots of activations (kXR) and codes (kCR): loaded two steps ahead (three slots of each; with one wave
-    // a SIMD the registers are there): 4096 x 4096 at M = 256 q4 23.6 -> 22.6 us, q8 31.1 -> 28.2 us against two
-    // slots (four measured no better for q8). Separate arrays: one array of the slots ends up in scratch.
-    constexpr int kXR = 3, kCR = 3;
+    // register slots of activations (kXR) and codes (kCR), each loaded kXR - 1 / kCR - 1 steps ahead (one wave a
+    // SIMD: the registers are there). 4096 x 4096 at M = 256 against two of each: q4 three activation and two code
+    // slots 23.6 -> 22.1 us (three code slots too: 22.6 us and a 36-byte spill a lane), q8 three of each 31.1 ->
+    // 28.2 us (four no better). Separate arrays: one array of the slots ends up in scratch.
+    constexpr int kXR = 3, kCR = BITS == 8 ? 3 : 2;
     uint4 xa0[kChunks], xa1[kChunks], xa2[kChunks];  // [load]: activations as loaded, slots 0..2
     uint4 cw[kCR][2][2];  // [slot][nb][half]: codes
     auto issue = [&](int q, int slot) __attribute__((always_inline)) {
