@@ -23,6 +23,11 @@ METRIC = "µs/layer for q4 MoE verify at M=6 + achieved HBM GB/s; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
 ROTATE_BYTES = 1_100_000_000  # weight replicas rotated by the dense GEMV lines: > 4x the 256 MB Infinity Cache
 TRAFFIC_JSON = os.path.join("profiles", "hbm_traffic.json")
+TRAFFIC_GEMV_JSON = os.path.join("profiles", "hbm_traffic_gemv.json")
+# configs 1 and 2: (name, bits, N, K, G, M, activation dtype name)
+GEMV_CONFIGS = (("cfg1_q4_4096x4096_M1_f32", 4, 4096, 4096, 128, 1, "float32"),
+                ("cfg2_q4_12288x4096_M6", 4, 12288, 4096, 128, 6, "bfloat16"),
+                ("cfg2_q8_12288x4096_M6", 8, 12288, 4096, 64, 6, "bfloat16"))
 COPY_PROBE_BYTES = 256 << 20  # FP32 elements read and written once by the calibration kernel
 
 
@@ -51,6 +56,10 @@ def parse():
                     help="only the streaming-read and MFMA probes (for rocprofv3 runs): one JSON line")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two --probe counter runs (FETCH_SIZE, WRITE_SIZE) into " + TRAFFIC_JSON)
+    ap.add_argument("--probe-gemv", action="store_true",
+                    help="for rocprofv3 --pmc: the copy kernel, then configs 1 and 2 over their rotated replicas")
+    ap.add_argument("--pmc-summary-gemv", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two --probe-gemv counter runs into " + TRAFFIC_GEMV_JSON)
     return ap.parse_args()
 
 
@@ -370,9 +379,8 @@ def verify_gemv():
     from strixite_amd import synthetic as syn
 
     res = {}
-    for name, bits, N, K, G, M, act in (("cfg1_q4_4096x4096_M1_f32", 4, 4096, 4096, 128, 1, torch.float32),
-                                        ("cfg2_q4_12288x4096_M6", 4, 12288, 4096, 128, 6, torch.bfloat16),
-                                        ("cfg2_q8_12288x4096_M6", 8, 12288, 4096, 64, 6, torch.bfloat16)):
+    for name, bits, N, K, G, M, act in GEMV_CONFIGS:
+        act = getattr(torch, act)
         one = N * K * bits // 8 + 4 * N * (K // G)
         reps = [syn.qweight(bits, N, K, G, seed=30 + i) for i in range(-(-ROTATE_BYTES // one))]
         x = syn.activations(M, K, seed=40, dtype=act)
@@ -511,12 +519,7 @@ def probe():
     from strixite_amd import synthetic as syn
     from strixite_amd.verify import MoeVerifyLayer
 
-    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
-    dst = torch.empty_like(src)
-    for _ in range(5):
-        torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads src, writes dst
-    torch.cuda.synchronize()
-    del src, dst
+    copy_probe()
     E, d, I, k, M, R = 512, 4096, 1024, 10, 6, 16
     Wr = syn.router_weight(E, d, seed=11)
     gu = syn.qweight(4, E * 2 * I, d, 128, seed=12)
@@ -550,9 +553,49 @@ def probe():
     print(json.dumps({"probe": "done", "algorithmic_bytes_per_launch": alg, "distinct_experts": Us}))
 
 
-def pmc_summary(fetch_dir, write_dir):
+def copy_probe():
+    """The counters' calibration: one elementwise kernel that reads and writes COPY_PROBE_BYTES, five times."""
+    import torch
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads src, writes dst
+    torch.cuda.synchronize()
+
+
+def probe_gemv():
+    """The copy kernel, then configs 1 and 2 each once over all their rotated replicas (every launch a replica not
+    read before in the run). Run under rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE)."""
+    import torch
+
+    from strixite_amd import kernels as kx
+    from strixite_amd import synthetic as syn
+
+    copy_probe()
+    alg = {}
+    for name, bits, N, K, G, M, act in GEMV_CONFIGS:
+        reps = [syn.qweight(bits, N, K, G, seed=30 + i) for i in range(-(-ROTATE_BYTES // (N * K * bits // 8 + 4 * N * (K // G))))]
+        x = syn.activations(M, K, seed=40, dtype=getattr(torch, act))
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        for w in reps:
+            kx.linear(x, w, out_act=0, y=y)
+        torch.cuda.synchronize()
+        alg[name] = reps[0].nbytes() + x.numel() * x.element_size() + y.numel() * 4
+        del reps
+        torch.cuda.empty_cache()
+    print(json.dumps({"probe": "done", "algorithmic_bytes_per_launch": alg}))
+
+
+# dense_ks_kernel instantiations of configs 1 and 2 (alone in a --probe-gemv run)
+GEMV_KERNELS = (("cfg1_q4_4096x4096_M1_f32", "dense_ks_kernel<4, 3, 4, 1, float, float, false>"),
+                ("cfg2_q4_12288x4096_M6", "dense_ks_kernel<4, 1, 4, 1, unsigned short, float, false>"),
+                ("cfg2_q8_12288x4096_M6", "dense_ks_kernel<8, 1, 8, 1, unsigned short, float, false>"))
+
+
+def pmc_summary(fetch_dir, write_dir, gemv=False):
     """Per-launch HBM traffic of the probe's kernels from two rocprofv3 counter runs, each scaled by what the same
-    counter reads for the copy kernel (COPY_PROBE_BYTES read and written)."""
+    counter reads for the copy kernel (COPY_PROBE_BYTES read and written). gemv: a --probe-gemv run (configs 1 and 2)."""
     import csv
     import glob
 
@@ -565,10 +608,13 @@ def pmc_summary(fetch_dir, write_dir):
                 name, v = r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0  # KiB -> bytes
                 if "MulFunctor" in name:
                     copies.append((int(r["Grid_Size"]), v))
-                key = ("gg_down" if "gg_down_kernel" in name else "gg_gate_up" if "gg_kernel" in name
-                       else "combine_reduce" if "combine_reduce" in name else "lm_head" if "dense_ks_kernel" in name
-                       else "verify_tail" if "topk_accept_kernel" in name else "gate_up" if "gate_up_kernel" in name
-                       else "down" if "down_kernel" in name else None)
+                if gemv:
+                    key = next((k for k, inst in GEMV_KERNELS if inst in name), None)
+                else:
+                    key = ("gg_down" if "gg_down_kernel" in name else "gg_gate_up" if "gg_kernel" in name
+                           else "combine_reduce" if "combine_reduce" in name else "lm_head" if "dense_ks_kernel" in name
+                           else "verify_tail" if "topk_accept_kernel" in name else "gate_up" if "gate_up_kernel" in name
+                           else "down" if "down_kernel" in name else None)
                 if key:
                     rows.setdefault(key, []).append(v)
         big = max(g for g, _ in copies)  # the copy probe: the largest multiply launched
@@ -580,14 +626,16 @@ def pmc_summary(fetch_dir, write_dir):
     out = {"copy_probe_bytes": COPY_PROBE_BYTES, "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
            "note": "FETCH_SIZE / WRITE_SIZE (KiB a dispatch) times the factor that makes the copy kernel read and "
                    "write exactly copy_probe_bytes"}
-    for k in ("gate_up", "down", "gg_gate_up", "gg_down", "combine_reduce", "lm_head", "verify_tail"):
+    keys = [k for k, _ in GEMV_KERNELS] if gemv else ["gate_up", "down", "gg_gate_up", "gg_down", "combine_reduce",
+                                                        "lm_head", "verify_tail"]
+    for k in keys:
         if k not in fetch or k not in write:
             continue
         fb, wb = fetch[k] * f_scale, write[k] * w_scale
         out[k] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "hbm_bytes_per_launch": int(fb + wb),
                   "raw_fetch_kib": round(fetch[k] / 1024, 1), "raw_write_kib": round(write[k] / 1024, 1)}
     os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
-    with open(os.path.join(ROOT, TRAFFIC_JSON), "w") as f:
+    with open(os.path.join(ROOT, TRAFFIC_GEMV_JSON if gemv else TRAFFIC_JSON), "w") as f:
         json.dump(out, f, indent=1)
     print(json.dumps(out))
 
@@ -596,6 +644,9 @@ def main():
     args = parse()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.pmc_summary_gemv:
+        pmc_summary(*args.pmc_summary_gemv, gemv=True)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported (multi-GPU is a "
@@ -607,6 +658,9 @@ def main():
     strixite_amd.lib()  # fails loudly without the built library
     if args.probe:
         probe()
+        return
+    if args.probe_gemv:
+        probe_gemv()
         return
     if args.prefill_only:
         print(json.dumps({"cfg4_prefill_layer": prefill_layer()}))
